@@ -1,0 +1,88 @@
+/*
+ * fa2_fwd.h - C ABI of the gfx950 (MI355X) FlashAttention-2 forward.
+ *
+ * The reference (roy6n23/triton-fa2-forward) reaches its GPU through one Triton launch,
+ * `_attn_fwd[grid](q, k, v, out, 16 strides, H_Q, N_Q, N_KV, qk_scale, constexprs...)`
+ * at fa2/kernel.py:247-259, and keeps its host policy in Python
+ * (`_default_config` fa2/kernel.py:186-195, `should_pack_gqa` fa2/kernel.py:198-207).
+ * This header is what a host binds instead: plain pointers, element strides and sizes,
+ * no torch types. Device buffers are owned by the caller; the library allocates nothing
+ * per call and keeps no per-call state. Launches are asynchronous on the given stream.
+ *
+ * Return convention: 0 on success, a negative FA2_E* code on a rejected argument or a
+ * failed launch; fa2_last_error() then describes the failure (thread-local string).
+ */
+#ifndef FA2_FWD_H
+#define FA2_FWD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of q, k, v and out (all four share it), fa2/kernel.py:222. */
+#define FA2_DTYPE_F16 0
+#define FA2_DTYPE_BF16 1
+
+#define FA2_OK 0
+#define FA2_EINVAL (-1)      /* an argument violates the contract below */
+#define FA2_EALIGN (-2)      /* a pointer or stride breaks the 16-byte load rule */
+#define FA2_ELAUNCH (-3)     /* the HIP launch itself failed */
+
+/*
+ * fa2_attn_fwd - out = softmax(q k^T * sm_scale [+ top-left causal mask]) v, fused.
+ *
+ * Replaces the launch `_attn_fwd[grid](...)` (fa2/kernel.py:247-259), with the kernel
+ * `_attn_fwd` (fa2/kernel.py:110-183) and its loop `_attn_fwd_inner` (fa2/kernel.py:60-107).
+ *
+ *   q, out   [batch, h_q,  n_q,  head_dim]   device pointers
+ *   k, v     [batch, h_kv, n_kv, head_dim]
+ *   *_stride element strides in [b, h, n, d] order; the d stride must be 1, the others
+ *            multiples of 8 elements, and every base pointer 16-byte aligned (FA2_EALIGN).
+ *   head_dim in {16, 32, 64, 128};  h_q % h_kv == 0;  causal implies n_q == n_kv
+ *            (fa2/kernel.py:218-228).
+ *   dtype    FA2_DTYPE_F16 or FA2_DTYPE_BF16.
+ *   pack     1, or the GQA group h_q / h_kv: that many query heads share one program
+ *            (fa2/kernel.py:233-238); block_m must then be a multiple of pack.
+ *   block_m  rows of (position, head) pairs per program, 1..256 (fa2/kernel.py:135-137).
+ *   block_n  keys per K/V tile; 0 takes the default. The kernel streams K/V in tiles of
+ *            32, 64 or 128 keys and rounds block_n up to the next of these.
+ *   qk_scale sm_scale * log2(e) > 0 (fa2/kernel.py:240-244).
+ *   stream   a hipStream_t (NULL = the default stream of the current device).
+ */
+int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                 const int64_t q_stride[4], const int64_t k_stride[4],
+                 const int64_t v_stride[4], const int64_t o_stride[4],
+                 int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                 int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                 int32_t block_m, int32_t block_n, float qk_scale, void* stream);
+
+/*
+ * fa2_default_config - the gfx950 tile configuration for a head dim.
+ * Replaces `_default_config(head_dim, on_cuda)` (fa2/kernel.py:186-195). Writes
+ * block_m (rows per program), block_n (keys per K/V tile), num_waves (wave64s per
+ * workgroup, the counterpart of Triton's num_warps) and num_stages (K/V buffers in
+ * flight). Returns FA2_EINVAL for an unsupported head_dim.
+ */
+int fa2_default_config(int32_t head_dim, int32_t* block_m, int32_t* block_n,
+                       int32_t* num_waves, int32_t* num_stages);
+
+/*
+ * fa2_should_pack_gqa - FlashAttention-3's packing rule, as `should_pack_gqa`
+ * (fa2/kernel.py:198-207): 1 when group > 1, block_m % group == 0 and the unpacked
+ * tiles are less than 90% as full as the packed ones; else 0.
+ */
+int fa2_should_pack_gqa(int32_t n_q, int32_t group, int32_t block_m);
+
+/* Thread-local description of the last failure in this thread ("" if none). */
+const char* fa2_last_error(void);
+
+/* Library version string, including the gfx target it was built for. */
+const char* fa2_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA2_FWD_H */

@@ -1,0 +1,180 @@
+"""CPU tests of the host side: the drop-in's policy and errors, and the C ABI of libfa2_fwd.so.
+
+None of these launch a kernel. The C-ABI calls here all stop at argument checking (or at the
+empty-output early return), which touches no GPU.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from fa2 import _lib
+from fa2.kernel import _default_config, attention, should_pack_gqa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fa2_fwd.h")
+
+needs_lib = pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH),
+                               reason="libfa2_fwd.so not built (python triton-fa2-forward_amd/csrc/build.py)")
+
+
+def cpu_qkv(B, H_q, H_kv, N_q, N_kv, D, dtype=torch.float16):
+    g = torch.Generator().manual_seed(0)
+    return (torch.randn(B, H_q, N_q, D, generator=g).to(dtype),
+            torch.randn(B, H_kv, N_kv, D, generator=g).to(dtype),
+            torch.randn(B, H_kv, N_kv, D, generator=g).to(dtype))
+
+
+# ------------------------------------------------------------------------------------------
+# policy (fa2/kernel.py:186-207) and the reference's known answers
+# ------------------------------------------------------------------------------------------
+
+def test_should_pack_gqa_follows_tile_efficiency():
+    """tests/test_correctness.py:271-280, verbatim known answers."""
+    assert should_pack_gqa(1, 4, 128)
+    assert should_pack_gqa(64, 4, 128)
+    assert not should_pack_gqa(4096, 4, 128)
+    assert not should_pack_gqa(1000, 4, 128)
+    assert not should_pack_gqa(64, 1, 128)
+    assert not should_pack_gqa(64, 3, 128)
+
+
+def test_should_pack_gqa_c5_does_not_pack_by_rule():
+    # BASELINE C5 (group 7, N=1000): 128 % 7 != 0, and even at block_m 112 the rule says no
+    assert not should_pack_gqa(1000, 7, 128)
+    assert not should_pack_gqa(1000, 7, 112)
+    assert should_pack_gqa(1, 7, 112)
+
+
+def test_default_config_table():
+    for d in (16, 32, 64, 128):
+        bm, bn, nw, ns = _default_config(d, True)
+        assert bm % 32 == 0 and bn in (32, 64, 128) and nw == bm // 32 and ns >= 1
+    assert _default_config(64, False) == (32, 16, 1, 1)
+
+
+# ------------------------------------------------------------------------------------------
+# the reference's argument errors, raised before anything reaches the GPU
+# ------------------------------------------------------------------------------------------
+
+def test_pack_gqa_needs_block_m_divisible_by_group():
+    q, k, v = cpu_qkv(1, 6, 2, 16, 16, 64)     # group 3 does not divide BLOCK_M
+    with pytest.raises(ValueError, match="BLOCK_M"):
+        attention(q, k, v, causal=True, pack_gqa=True)
+
+
+def test_sm_scale_must_be_positive():
+    q, k, v = cpu_qkv(1, 4, 2, 16, 16, 64)
+    with pytest.raises(ValueError, match="sm_scale"):
+        attention(q, k, v, sm_scale=-0.125)
+    with pytest.raises(ValueError, match="sm_scale"):
+        attention(q, k, v, sm_scale=0.0)
+
+
+@pytest.mark.parametrize("bad", ["rank", "dtype", "head_dim", "gqa", "causal_lengths", "kv_shape"])
+def test_shape_and_dtype_assertions(bad):
+    q, k, v = cpu_qkv(1, 4, 2, 16, 16, 64)
+    if bad == "rank":
+        q = q[0]
+    elif bad == "dtype":
+        q, k, v = q.float(), k.float(), v.float()
+    elif bad == "head_dim":
+        q, k, v = (t[..., :48].contiguous() for t in (q, k, v))
+    elif bad == "gqa":
+        q = torch.cat([q, q[:, :1]], dim=1)    # 5 query heads over 2 KV heads
+    elif bad == "causal_lengths":
+        k, v = k[:, :, :8], v[:, :, :8]
+    elif bad == "kv_shape":
+        v = v[:, :, :8]
+    with pytest.raises(AssertionError):
+        attention(q, k, v, causal=True)
+
+
+def test_cpu_tensors_fail_loudly():
+    """No silent CPU or PyTorch fallback exists on the product path."""
+    q, k, v = cpu_qkv(1, 4, 2, 16, 16, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        attention(q, k, v, causal=True)
+
+
+# ------------------------------------------------------------------------------------------
+# the C ABI: load, exports, policy agreement, argument checks
+# ------------------------------------------------------------------------------------------
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(fa2_[a-z0-9_]+)\s*\(", text))
+
+
+@needs_lib
+def test_library_exports_every_declared_symbol():
+    declared = _declared_functions()
+    assert {"fa2_attn_fwd", "fa2_default_config", "fa2_should_pack_gqa",
+            "fa2_last_error", "fa2_version"} <= declared
+    lib = _lib.lib()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(_lib.SIGNATURES) == declared
+    assert b"gfx950" in lib.fa2_version()
+
+
+@needs_lib
+def test_c_policy_matches_python():
+    lib = _lib.lib()
+    for n_q in (1, 3, 16, 64, 100, 1000, 4096):
+        for group in (1, 2, 3, 4, 7, 8, 32):
+            for bm in (16, 32, 64, 112, 128, 256):
+                assert bool(lib.fa2_should_pack_gqa(n_q, group, bm)) == should_pack_gqa(n_q, group, bm)
+    for d in (16, 32, 64, 128):
+        out = [ctypes.c_int32() for _ in range(4)]
+        assert lib.fa2_default_config(d, *(ctypes.byref(o) for o in out)) == 0
+        assert tuple(o.value for o in out) == _default_config(d, True)
+    assert lib.fa2_default_config(48, None, None, None, None) == -1
+
+
+def _call(**over):
+    """fa2_attn_fwd with valid defaults except `over`; pointers are fake (16-byte aligned)."""
+    a = dict(q=0x1000, k=0x2000, v=0x3000, out=0x4000, sq=(8192, 2048, 64, 1), sk=(4096, 2048, 64, 1),
+             sv=(4096, 2048, 64, 1), so=(8192, 2048, 64, 1), batch=1, h_q=4, h_kv=2, n_q=32, n_kv=32,
+             head_dim=64, dtype=0, causal=1, pack=1, block_m=128, block_n=64, qk_scale=0.18, stream=None)
+    a.update(over)
+    arr = lambda s: (ctypes.c_int64 * 4)(*s)  # noqa: E731
+    lib = _lib.lib()
+    rc = lib.fa2_attn_fwd(a["q"], a["k"], a["v"], a["out"], arr(a["sq"]), arr(a["sk"]), arr(a["sv"]),
+                          arr(a["so"]), a["batch"], a["h_q"], a["h_kv"], a["n_q"], a["n_kv"],
+                          a["head_dim"], a["dtype"], a["causal"], a["pack"], a["block_m"], a["block_n"],
+                          a["qk_scale"], a["stream"])
+    return rc, _lib.last_error()
+
+
+@needs_lib
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(head_dim=48), -1, "head_dim"),
+    (dict(h_q=5), -1, "divisible"),
+    (dict(dtype=2), -1, "dtype"),
+    (dict(n_kv=16), -1, "N_q == N_kv"),
+    (dict(pack=3), -1, "pack"),
+    (dict(pack=2, block_m=127), -1, "BLOCK_M"),
+    (dict(block_m=0), -1, "BLOCK_M"),
+    (dict(block_m=257), -1, "BLOCK_M"),
+    (dict(block_n=129), -1, "BLOCK_N"),
+    (dict(qk_scale=0.0), -1, "qk_scale"),
+    (dict(qk_scale=-1.0), -1, "qk_scale"),
+    (dict(q=0x1008), -2, "aligned"),
+    (dict(sq=(8192, 2048, 64, 2)), -2, "stride"),
+    (dict(sk=(4096, 2048, 60, 1)), -2, "multiples of 8"),
+    (dict(q=0), -1, "null"),
+])
+def test_c_abi_rejects_bad_arguments(over, code, msg):
+    rc, err = _call(**over)
+    assert rc == code and msg in err, (rc, err)
+
+
+@needs_lib
+def test_c_abi_empty_output_is_a_no_op():
+    assert _call(batch=0, q=0, k=0, v=0, out=0)[0] == 0
+    assert _call(n_q=0, n_kv=0, q=0, k=0, v=0, out=0)[0] == 0

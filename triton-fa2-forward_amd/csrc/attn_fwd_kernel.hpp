@@ -1,0 +1,350 @@
+// attn_fwd_kernel.hpp - the gfx950 FlashAttention-2 forward kernel.
+//
+// Computes what `_attn_fwd` / `_attn_fwd_inner` compute (fa2/kernel.py:60-183):
+//   O = softmax(Q K^T * sm_scale [+ top-left causal mask]) V
+// with the online softmax in base 2 (exp2, qk_scale = sm_scale * log2 e folded into one
+// FMA per score, fa2/kernel.py:95-97), two-stage causal skipping (fa2/kernel.py:150-169),
+// GQA by index mapping and optional head packing (fa2/kernel.py:126-141).
+//
+// CDNA4 mapping (one workgroup = one program of the reference):
+//   * NW wave64s, each owning 32 consecutive rows of the program's block_m rows.
+//   * Each wave computes the TRANSPOSED score block S^T = K Q^T with
+//     v_mfma_f32_32x32x16_{bf16,f16}: K (32 keys x 16 dims) is the A operand, read
+//     from LDS; Q^T is the B operand and stays in VGPRs for the whole loop.
+//     In the 32x32 accumulator, lane l holds column l%32 (= one query row) and 16 of the
+//     32 keys; the other 16 keys of that row sit in lane l^32. A row's max and sum are
+//     therefore 16-value lane-local reductions plus one v_permlane32_swap.
+//   * K rows are fed to the A operand in the order pi(r) (bits 2 and 3 of r swapped),
+//     which makes accumulator register i of lane l hold key 16*(i/8) + 8*(l/32) + i%8.
+//     Registers 8h..8h+7 are then 8 consecutive keys, i.e. exactly the B operand
+//     (P^T, 8 consecutive k) of the second product O^T += V^T P^T: P never leaves VGPRs.
+//   * V stays in its HBM layout [key][dim] in LDS and is read as the A operand V^T with
+//     ds_read_b64_tr_b16 (gfx950's transposing LDS read): each 16-lane group reads a
+//     4-key x 16-dim block and every lane receives 4 consecutive keys of one dim.
+//   * O^T accumulates in 32x32 blocks whose lane l holds column l%32 = the lane's own
+//     query row, so the per-row rescale by alpha is a lane-local multiply.
+//   * K/V tiles are double buffered through registers: the next tile's global loads are
+//     in flight while the current tile's MFMAs run from LDS.
+//   * LDS layouts are XOR-swizzled at 16-byte granularity so that both the b128 reads
+//     of K and the transposing b64 reads of V are free of bank conflicts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_fwd_params.hpp"
+
+namespace fa2 {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+#define FA2_LDS __attribute__((address_space(3)))
+
+// ---------------------------------------------------------------------------------
+// element type traits: the MFMA and the fp32 -> 16-bit pair conversion (RNE)
+// ---------------------------------------------------------------------------------
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<0> {  // fp16
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    f16x2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+template <>
+struct Elem<1> {  // bf16
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+// ---------------------------------------------------------------------------------
+// index helpers
+// ---------------------------------------------------------------------------------
+
+// Swap bits 2 and 3 of a row index inside a 32-row block (an involution).
+__device__ __forceinline__ constexpr int pi_row(int x) {
+  return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1);
+}
+
+// XOR key of the K tile's 16-byte chunks. u = pi_row(row % 32) % 16, i.e. the lane index
+// (mod 16) that reads this row. Chosen (exhaustive search over linear keys) so that the
+// b128 A-operand reads are conflict-free for 32- and 64-bank LDS models.
+template <int D>
+__device__ __forceinline__ int k_key(int u) {
+  if constexpr (D == 128) {
+    return u & 15;
+  } else if constexpr (D == 64) {
+    return ((u >> 1) & 1) | (((u >> 2) & 1) << 1) | (((u ^ (u >> 3)) & 1) << 2);
+  } else if constexpr (D == 32) {
+    return ((u >> 2) & 1) | ((((u >> 1) ^ (u >> 3)) & 1) << 1);
+  } else {
+    return (u >> 2) & 1;
+  }
+}
+
+// XOR key of the V tile's 16-byte chunks, a function of the key row (mod 16); makes the
+// ds_read_b64_tr_b16 reads conflict-free for 32- and 64-bank LDS models.
+template <int D>
+__device__ __forceinline__ int v_key(int row) {
+  if constexpr (D == 128) {
+    return ((row & 1) << 1) | ((row & 2) << 1) | ((row & 1) << 3);
+  } else if constexpr (D == 64) {
+    return ((row & 1) << 1) | ((row & 2) << 1);
+  } else if constexpr (D == 32) {
+    return row & 2;
+  } else {
+    return 0;
+  }
+}
+
+// max / sum of a value over the lane pair (l, l^32)
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ u32x2 lds_read_tr(const char FA2_LDS* p) {
+  i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 FA2_LDS*)p);
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// ---------------------------------------------------------------------------------
+// the kernel
+// ---------------------------------------------------------------------------------
+template <int DT, int D, int NW, int BN, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
+  using E = Elem<DT>;
+  constexpr int NT = NW * 64;
+  constexpr int KS = D / 16;               // 16-dim k-steps of S^T = K Q^T
+  constexpr int DB = (D + 31) / 32;        // 32-dim row blocks of O^T
+  constexpr int NB = BN / 32;              // 32-key row blocks of S^T
+  constexpr int CPR = D / 8;               // 16-byte chunks per K / V row
+  constexpr int TCH = BN * CPR;            // chunks per K (or V) tile
+  constexpr int LPT = (TCH + NT - 1) / NT; // chunks each thread moves per tile
+
+  __shared__ u32x4 k_lds[TCH];
+  __shared__ u32x4 v_lds[TCH];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int c = lane & 31;
+  const int g = lane >> 5;
+
+  // ---- which program am I (fa2/kernel.py:126-130)? Causal programs are issued
+  // heaviest (last) q-tile first so the short ones fill the tail.
+  const int bh = blockIdx.x % p.n_bh;
+  const int tq = blockIdx.x / p.n_bh;
+  const int tile = CAUSAL ? p.n_tiles - 1 - tq : tq;
+  const int heads_per_prog = p.h_q / p.pack;
+  const int b = bh / heads_per_prog;
+  const int hq0 = (bh - b * heads_per_prog) * p.pack;
+  const int hkv = hq0 / p.group;
+
+  // ---- this lane's query row: packed row r -> (position r / pack, head r % pack)
+  // (fa2/kernel.py:135-139). Rows past block_m or past n_q compute on zeros and are
+  // never stored; they see every key so their softmax stays finite.
+  const int lrow = wave * 32 + c;
+  const int r = tile * p.block_m + lrow;
+  const int pos = r / p.pack;
+  const int head = hq0 + (r - pos * p.pack);
+  const bool row_ok = lrow < p.block_m && pos < p.n_q;
+  const int pos_vis = row_ok ? pos : 0x3fffffff;
+
+  // ---- Q^T operand, loaded once (fa2/kernel.py:144)
+  u32x4 qreg[KS];
+  {
+    const uint16_t* qrow = p.q + b * p.sqb + head * p.sqh + (int64_t)pos * p.sqn + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qreg[ks] = row_ok ? *(const u32x4*)(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // ---- key range (fa2/kernel.py:150-175). Tiles below full_end need no mask:
+  // causal: every column left of the tile's first position (stage 1, rounded down to
+  // a whole tile); full: every whole tile. The rest is masked (stage 2 / the tail).
+  const int pos_per_prog = p.block_m / p.pack;
+  const int lo_pos = tile * pos_per_prog;
+  int kv_end, full_end;
+  if (CAUSAL) {
+    kv_end = min(lo_pos + pos_per_prog, p.n_kv);
+    full_end = (lo_pos / BN) * BN;
+  } else {
+    kv_end = p.n_kv;
+    full_end = (p.n_kv / BN) * BN;
+  }
+
+  const uint16_t* kbase = p.k + b * p.skb + hkv * p.skh;
+  const uint16_t* vbase = p.v + b * p.svb + hkv * p.svh;
+
+  // ---- K/V staging: global -> registers (next tile) -> LDS (current tile)
+  u32x4 kr[LPT], vr[LPT];
+  auto gload = [&](int n0) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int ci = tid + i * NT;
+      if (TCH % NT == 0 || ci < TCH) {
+        const int row = ci / CPR, col = ci % CPR;
+        const int n = n0 + row;
+        const bool ok = n < p.n_kv;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        kr[i] = ok ? *(const u32x4*)(kbase + (int64_t)n * p.skn + col * 8) : z;
+        vr[i] = ok ? *(const u32x4*)(vbase + (int64_t)n * p.svn + col * 8) : z;
+      }
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int ci = tid + i * NT;
+      if (TCH % NT == 0 || ci < TCH) {
+        const int row = ci / CPR, col = ci % CPR;
+        k_lds[row * CPR + (col ^ k_key<D>(pi_row(row & 31) & 15))] = kr[i];
+        v_lds[row * CPR + (col ^ v_key<D>(row & 15))] = vr[i];
+      }
+    }
+  };
+
+  // per-lane LDS offsets that do not change across tiles
+  const int kk = k_key<D>(c & 15);
+  const int vs = lane & 15;          // role inside the 16-lane transpose group
+  const int vj = vs >> 2;            // key row within the 4-row block it addresses
+  const int vq = vs & 3;
+  const int vsig = ((vq & 1) << 1) | ((vq & 2) >> 1);
+  const int vdh = (D == 16) ? 0 : ((lane >> 4) & 1);
+  const char FA2_LDS* v_lds_b = (const char FA2_LDS*)v_lds;
+
+  // ---- online-softmax state (fa2/kernel.py:146-148); l is a per-lane partial sum
+  float m_i = -INFINITY;
+  float l_i = 0.f;
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+
+  const float qk_scale = p.qk_scale;
+
+  auto step = [&]<bool MASK>(int n0) {
+    // S^T = K Q^T  (fa2/kernel.py:75-79)
+    f32x16 s[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) s[nb] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const u32x4 a = k_lds[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + g) ^ kk)];
+        s[nb] = E::mma(a, qreg[ks], s[nb]);
+      }
+    }
+    // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos.
+    if constexpr (MASK) {
+      const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (nb * 32 + 16 * (i / 8) + (i % 8) > lim) s[nb][i] = -INFINITY;
+    }
+    // online softmax in base 2 (fa2/kernel.py:95-98)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
+    mx = pair_max(mx);
+    const float m_new = fmaxf(m_i, mx * qk_scale);
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+    float rs = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][i], qk_scale, -m_new));
+        s[nb][i] = e;
+        rs += e;
+      }
+    l_i = l_i * alpha + rs;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    m_i = m_new;
+    // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
+#pragma unroll
+    for (int t = 0; t < BN / 16; ++t) {
+      const int nb = t >> 1, h = t & 1;
+      const u32x4 pb = {E::pack2(s[nb][8 * h + 0], s[nb][8 * h + 1]),
+                        E::pack2(s[nb][8 * h + 2], s[nb][8 * h + 3]),
+                        E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
+                        E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        u32x2 part[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int row = 16 * t + 8 * g + 4 * rr + vj;
+          const int chunk = (4 * db + 2 * vdh + (vsig >> 1)) ^ v_key<D>(row & 15);
+          part[rr] = lds_read_tr(v_lds_b + row * (D * 2) + chunk * 16 + (vsig & 1) * 8);
+        }
+        const u32x4 a = {part[0][0], part[0][1], part[1][0], part[1][1]};
+        acc[db] = E::mma(a, pb, acc[db]);
+      }
+    }
+  };
+
+  // ---- main loop: prefetch tile j+1 into registers while tile j computes from LDS
+  if (0 < kv_end) gload(0);
+  for (int n0 = 0; n0 < kv_end; n0 += BN) {
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (n0 + BN < kv_end) gload(n0 + BN);
+    if (n0 + BN <= full_end)
+      step.template operator()<false>(n0);
+    else
+      step.template operator()<true>(n0);
+  }
+
+  // ---- normalise once, store once (fa2/kernel.py:178-183)
+  const float l = pair_sum(l_i);
+  if (row_ok) {
+    uint16_t* orow = p.o + b * p.sob + head * p.soh + (int64_t)pos * p.son;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int d0 = 32 * db + 16 * h + 8 * g;
+        if (d0 < D) {
+          const u32x4 o = {E::pack2(acc[db][8 * h + 0] / l, acc[db][8 * h + 1] / l),
+                           E::pack2(acc[db][8 * h + 2] / l, acc[db][8 * h + 3] / l),
+                           E::pack2(acc[db][8 * h + 4] / l, acc[db][8 * h + 5] / l),
+                           E::pack2(acc[db][8 * h + 6] / l, acc[db][8 * h + 7] / l)};
+          *(u32x4*)(orow + d0) = o;
+        }
+      }
+  }
+}
+
+}  // namespace fa2

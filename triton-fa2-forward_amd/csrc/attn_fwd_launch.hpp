@@ -1,0 +1,32 @@
+// attn_fwd_launch.hpp - per (dtype, head_dim) launchers of the forward kernel.
+//
+// Each instantiation lives in its own translation unit (attn_fwd_inst.hip compiled once per
+// dtype x head_dim), so the library's many kernel instances build in parallel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "attn_fwd_params.hpp"
+
+namespace fa2 {
+
+// Launches attn_fwd_kernel<DT, D, waves, block_n, causal> on `grid` programs.
+// waves in {1, 2, 4, 8}, block_n in {32, 64, 128}. Returns a hipError_t value.
+template <int DT, int D>
+int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsigned grid,
+                    hipStream_t stream);
+
+#define FA2_DECLARE_LAUNCH(DT, D)                                                          \
+  extern template int launch_attn_fwd<DT, D>(const Params&, int, int, bool, unsigned, \
+                                             hipStream_t);
+FA2_DECLARE_LAUNCH(0, 16)
+FA2_DECLARE_LAUNCH(0, 32)
+FA2_DECLARE_LAUNCH(0, 64)
+FA2_DECLARE_LAUNCH(0, 128)
+FA2_DECLARE_LAUNCH(1, 16)
+FA2_DECLARE_LAUNCH(1, 32)
+FA2_DECLARE_LAUNCH(1, 64)
+FA2_DECLARE_LAUNCH(1, 128)
+#undef FA2_DECLARE_LAUNCH
+
+}  // namespace fa2

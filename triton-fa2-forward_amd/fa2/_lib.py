@@ -1,0 +1,71 @@
+"""ctypes binding of libfa2_fwd.so, the C ABI declared in include/fa2_fwd.h.
+
+The library is built in-tree by triton-fa2-forward_amd/csrc/build.py and sits next to this
+file. torch is imported first so that its HIP runtime (SONAME libamdhip64.so.7) is the one
+already loaded when the library is opened: the library then launches on exactly the streams
+torch hands out.
+"""
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be loaded before the HIP library, see above)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfa2_fwd.so")
+
+# C-ABI symbols declared in include/fa2_fwd.h, with (restype, argtypes).
+_i32, _i64p, _vp = ctypes.c_int32, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p
+SIGNATURES = {
+    "fa2_attn_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
+                                    _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                    _i32, _i32, ctypes.c_float, _vp]),
+    "fa2_default_config": (ctypes.c_int, [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
+                                          ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
+    "fa2_should_pack_gqa": (ctypes.c_int, [_i32, _i32, _i32]),
+    "fa2_last_error": (ctypes.c_char_p, []),
+    "fa2_version": (ctypes.c_char_p, []),
+}
+
+DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1}
+
+_LIB = None
+
+
+def lib():
+    """The loaded library. Raises RuntimeError when it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing; build the HIP library first: "
+                "python triton-fa2-forward_amd/csrc/build.py")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = handle
+    return _LIB
+
+
+def last_error():
+    return lib().fa2_last_error().decode(errors="replace")
+
+
+def _strides(t):
+    # The stride of a size-1 dimension never enters an address; pass 0 so that only the
+    # strides the kernel actually steps by are checked against the 16-byte rule.
+    return (ctypes.c_int64 * 4)(*(0 if n == 1 else s for n, s in zip(t.shape, t.stride())))
+
+
+def attn_fwd(q, k, v, out, causal, pack, block_m, block_n, qk_scale, stream):
+    """Call fa2_attn_fwd on tensors that already satisfy the C contract."""
+    B, H_q, N_q, D = q.shape
+    H_kv, N_kv = k.shape[1], k.shape[2]
+    rc = lib().fa2_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+        _strides(q), _strides(k), _strides(v), _strides(out),
+        B, H_q, H_kv, N_q, N_kv, D, DTYPE_CODE[q.dtype], int(bool(causal)), pack,
+        block_m, block_n, qk_scale, stream)
+    if rc != 0:
+        raise RuntimeError(f"fa2_attn_fwd failed ({rc}): {last_error()}")
