@@ -7,7 +7,9 @@
 // GQA by index mapping and optional head packing (fa2/kernel.py:126-141).
 //
 // CDNA4 mapping (one workgroup = one program of the reference):
-//   * NW wave64s, each owning 32 consecutive rows of the program's block_m rows.
+//   * NW wave64s, each owning 32 consecutive rows of the program's block_m rows; the kernel
+//     is register-budgeted for two waves per SIMD so one wave's softmax overlaps another's
+//     matrix work.
 //   * Each wave computes the TRANSPOSED score block S^T = K Q^T with
 //     v_mfma_f32_32x32x16_{bf16,f16}: K (32 keys x 16 dims) is the A operand, read
 //     from LDS; Q^T is the B operand and stays in VGPRs for the whole loop.
@@ -23,10 +25,16 @@
 //     4-key x 16-dim block and every lane receives 4 consecutive keys of one dim.
 //   * O^T accumulates in 32x32 blocks whose lane l holds column l%32 = the lane's own
 //     query row, so the per-row rescale by alpha is a lane-local multiply.
-//   * K/V tiles are double buffered through registers: the next tile's global loads are
-//     in flight while the current tile's MFMAs run from LDS.
+//   * K/V tiles go HBM -> LDS directly (global_load_lds_dwordx4, no VGPR staging) into a
+//     double buffer: tile j+1 is in flight while tile j is consumed; one barrier per tile.
 //   * LDS layouts are XOR-swizzled at 16-byte granularity so that both the b128 reads
-//     of K and the transposing b64 reads of V are free of bank conflicts.
+//     of K and the transposing b64 reads of V are free of bank conflicts; the swizzle is
+//     applied by choosing which global chunk each lane fetches.
+//   * Lazy rescaling: a row's reference max only moves when the new max exceeds it by more
+//     than 2^8 (in exp2 units), so the O rescale (D/32 x 16 multiplies per lane) is skipped
+//     on most tiles. The result is the same softmax: acc and l share the reference.
+//   * Programs are ordered so that each XCD (its own L2) works through whole KV heads,
+//     heaviest causal tiles first.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -46,6 +54,12 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 #define FA2_LDS __attribute__((address_space(3)))
+#define FA2_GLOBAL __attribute__((address_space(1)))
+
+// Number of XCDs (each with its own L2) that the hardware deals workgroups to round-robin.
+constexpr int kXcds = 8;
+// Lazy-rescale threshold in exp2 units: the reference max lags the true max by at most this.
+constexpr float kRescaleTau = 8.0f;
 
 // ---------------------------------------------------------------------------------
 // element type traits: the MFMA and the fp32 -> 16-bit pair conversion (RNE)
@@ -132,22 +146,64 @@ __device__ __forceinline__ u32x2 lds_read_tr(const char FA2_LDS* p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// A raw buffer resource over [base, base + bytes): loads past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes HBM -> LDS without VGPRs: lane l of the wave writes lds_base + 16 * l.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
+                                           void FA2_LDS* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_base, 16, voffset, 0, 0, 0);
+}
+
+// The workgroup -> (q tile, batch, first query head) decomposition. Workgroups are dealt to
+// the XCDs round-robin; block b runs on XCD b % 8. Renumber so that each XCD receives a
+// contiguous range of "virtual" programs, ordered (batch, kv head) outermost, then q tile
+// (heaviest causal tile first), then the query-head groups sharing that KV head: an XCD's L2
+// then holds the K/V of the heads it is working on.
+struct Program {
+  int tile, b, hq0, hkv;
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ Program program_of(const Params& p, int block) {
+  const int total = p.n_tiles * p.n_bh;
+  const int q = total / kXcds, rem = total % kXcds;
+  const int xcd = block % kXcds, slot = block / kXcds;
+  const int v = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + slot;
+  const int progs_per_kv = p.group / p.pack;  // programs sharing one KV head per q tile
+  const int per_kv = p.n_tiles * progs_per_kv;
+  const int kv_index = v / per_kv;            // b * h_kv + hkv
+  const int r = v - kv_index * per_kv;
+  const int t = r / progs_per_kv;
+  const int h_in = r - t * progs_per_kv;
+  const int h_kv = p.h_q / p.group;
+  Program pr;
+  pr.tile = CAUSAL ? p.n_tiles - 1 - t : t;
+  pr.b = kv_index / h_kv;
+  pr.hkv = kv_index - pr.b * h_kv;
+  pr.hq0 = pr.hkv * p.group + h_in * p.pack;
+  return pr;
+}
+
 // ---------------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------------
 template <int DT, int D, int NW, int BN, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_fwd_kernel(const Params p) {
   using E = Elem<DT>;
-  constexpr int NT = NW * 64;
   constexpr int KS = D / 16;               // 16-dim k-steps of S^T = K Q^T
   constexpr int DB = (D + 31) / 32;        // 32-dim row blocks of O^T
   constexpr int NB = BN / 32;              // 32-key row blocks of S^T
   constexpr int CPR = D / 8;               // 16-byte chunks per K / V row
   constexpr int TCH = BN * CPR;            // chunks per K (or V) tile
-  constexpr int LPT = (TCH + NT - 1) / NT; // chunks each thread moves per tile
+  constexpr int NI = TCH / 64;             // 64-lane LDS load instructions per tile
+  static_assert(TCH % 64 == 0, "a tile must be whole 1 KiB load instructions");
 
-  __shared__ u32x4 k_lds[TCH];
-  __shared__ u32x4 v_lds[TCH];
+  __shared__ u32x4 k_lds[2][TCH];
+  __shared__ u32x4 v_lds[2][TCH];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -155,30 +211,22 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
   const int c = lane & 31;
   const int g = lane >> 5;
 
-  // ---- which program am I (fa2/kernel.py:126-130)? Causal programs are issued
-  // heaviest (last) q-tile first so the short ones fill the tail.
-  const int bh = blockIdx.x % p.n_bh;
-  const int tq = blockIdx.x / p.n_bh;
-  const int tile = CAUSAL ? p.n_tiles - 1 - tq : tq;
-  const int heads_per_prog = p.h_q / p.pack;
-  const int b = bh / heads_per_prog;
-  const int hq0 = (bh - b * heads_per_prog) * p.pack;
-  const int hkv = hq0 / p.group;
+  const Program pr = program_of<CAUSAL>(p, blockIdx.x);
 
   // ---- this lane's query row: packed row r -> (position r / pack, head r % pack)
   // (fa2/kernel.py:135-139). Rows past block_m or past n_q compute on zeros and are
   // never stored; they see every key so their softmax stays finite.
   const int lrow = wave * 32 + c;
-  const int r = tile * p.block_m + lrow;
+  const int r = pr.tile * p.block_m + lrow;
   const int pos = r / p.pack;
-  const int head = hq0 + (r - pos * p.pack);
+  const int head = pr.hq0 + (r - pos * p.pack);
   const bool row_ok = lrow < p.block_m && pos < p.n_q;
   const int pos_vis = row_ok ? pos : 0x3fffffff;
 
   // ---- Q^T operand, loaded once (fa2/kernel.py:144)
   u32x4 qreg[KS];
   {
-    const uint16_t* qrow = p.q + b * p.sqb + head * p.sqh + (int64_t)pos * p.sqn + 8 * g;
+    const uint16_t* qrow = p.q + pr.b * p.sqb + head * p.sqh + (int64_t)pos * p.sqn + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qreg[ks] = row_ok ? *(const u32x4*)(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
@@ -188,7 +236,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
   // causal: every column left of the tile's first position (stage 1, rounded down to
   // a whole tile); full: every whole tile. The rest is masked (stage 2 / the tail).
   const int pos_per_prog = p.block_m / p.pack;
-  const int lo_pos = tile * pos_per_prog;
+  const int lo_pos = pr.tile * pos_per_prog;
   int kv_end, full_end;
   if (CAUSAL) {
     kv_end = min(lo_pos + pos_per_prog, p.n_kv);
@@ -197,34 +245,35 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
     kv_end = p.n_kv;
     full_end = (p.n_kv / BN) * BN;
   }
+  const int n_tiles_kv = (kv_end + BN - 1) / BN;
 
-  const uint16_t* kbase = p.k + b * p.skb + hkv * p.skh;
-  const uint16_t* vbase = p.v + b * p.svb + hkv * p.svh;
-
-  // ---- K/V staging: global -> registers (next tile) -> LDS (current tile)
-  u32x4 kr[LPT], vr[LPT];
-  auto gload = [&](int n0) {
+  // ---- K/V staging: each wave issues every NW-th 1 KiB load of the tile. Chunk P of a tile
+  // (16 bytes, P = 64 * instruction + lane) holds row P / CPR, logical chunk
+  // (P % CPR) ^ key(row). The per-lane byte offsets are fixed; each tile moves the base of a
+  // buffer resource that ends after row n_kv - 1, so rows past the sequence read as zeros.
+  constexpr int JW = (NI + NW - 1) / NW;  // load instructions per wave per tensor
+  const char* kbase = (const char*)(p.k + pr.b * p.skb + pr.hkv * p.skh);
+  const char* vbase = (const char*)(p.v + pr.b * p.svb + pr.hkv * p.svh);
+  uint32_t koff[JW], voff[JW];
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int ci = tid + i * NT;
-      if (TCH % NT == 0 || ci < TCH) {
-        const int row = ci / CPR, col = ci % CPR;
-        const int n = n0 + row;
-        const bool ok = n < p.n_kv;
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        kr[i] = ok ? *(const u32x4*)(kbase + (int64_t)n * p.skn + col * 8) : z;
-        vr[i] = ok ? *(const u32x4*)(vbase + (int64_t)n * p.svn + col * 8) : z;
-      }
-    }
-  };
-  auto lstore = [&]() {
+  for (int jj = 0; jj < JW; ++jj) {
+    const int P = (wave + jj * NW) * 64 + lane;
+    const int row = P / CPR, col = P % CPR;
+    koff[jj] = (uint32_t)(row * p.skn + (col ^ k_key<D>(pi_row(row & 31) & 15)) * 8) * 2u;
+    voff[jj] = (uint32_t)(row * p.svn + (col ^ v_key<D>(row & 15)) * 8) * 2u;
+  }
+  auto issue_tile = [&](int n0, int buf) {
+    const int64_t rows_left = p.n_kv - n0;  // >= 1
+    const int64_t kbytes = ((rows_left - 1) * p.skn + D) * 2;
+    const int64_t vbytes = ((rows_left - 1) * p.svn + D) * 2;
+    const auto krs = make_rsrc(kbase + (int64_t)n0 * p.skn * 2, (uint32_t)min(kbytes, (int64_t)0x7fffffff));
+    const auto vrs = make_rsrc(vbase + (int64_t)n0 * p.svn * 2, (uint32_t)min(vbytes, (int64_t)0x7fffffff));
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int ci = tid + i * NT;
-      if (TCH % NT == 0 || ci < TCH) {
-        const int row = ci / CPR, col = ci % CPR;
-        k_lds[row * CPR + (col ^ k_key<D>(pi_row(row & 31) & 15))] = kr[i];
-        v_lds[row * CPR + (col ^ v_key<D>(row & 15))] = vr[i];
+    for (int jj = 0; jj < JW; ++jj) {
+      const int j = wave + jj * NW;
+      if (NI % NW == 0 || j < NI) {
+        load_lds16(krs, koff[jj], (void FA2_LDS*)&k_lds[buf][j * 64]);
+        load_lds16(vrs, voff[jj], (void FA2_LDS*)&v_lds[buf][j * 64]);
       }
     }
   };
@@ -236,7 +285,6 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
   const int vq = vs & 3;
   const int vsig = ((vq & 1) << 1) | ((vq & 2) >> 1);
   const int vdh = (D == 16) ? 0 : ((lane >> 4) & 1);
-  const char FA2_LDS* v_lds_b = (const char FA2_LDS*)v_lds;
 
   // ---- online-softmax state (fa2/kernel.py:146-148); l is a per-lane partial sum
   float m_i = -INFINITY;
@@ -247,21 +295,35 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
 
   const float qk_scale = p.qk_scale;
 
-  auto step = [&]<bool MASK>(int n0) {
-    // S^T = K Q^T  (fa2/kernel.py:75-79)
+  auto step = [&](int n0, int buf, bool masked) {
+    const u32x4 FA2_LDS* kt = (const u32x4 FA2_LDS*)k_lds[buf];
+    const char FA2_LDS* vt = (const char FA2_LDS*)v_lds[buf];
+    // S^T = K Q^T  (fa2/kernel.py:75-79); K operands are read one k-step ahead
     f32x16 s[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) s[nb] = f32x16{};
+    u32x4 ka[2][NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) ka[0][nb] = kt[(nb * 32 + pi_row(c)) * CPR + (g ^ kk)];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const u32x4 a = k_lds[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + g) ^ kk)];
-        s[nb] = E::mma(a, qreg[ks], s[nb]);
+        for (int nb = 0; nb < NB; ++nb)
+          ka[(ks + 1) & 1][nb] = kt[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + 2 + g) ^ kk)];
       }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s[nb] = E::mma(ka[ks & 1][nb], qreg[ks], s[nb]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);  // DS reads of the next k-step
+      __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);  // MFMAs of this k-step
     }
     // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos.
-    if constexpr (MASK) {
+    // `masked` is uniform over the workgroup; one copy of the tile code serves both cases
+    // so the accumulators keep one register assignment across the loop.
+    if (masked) {
       const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -269,68 +331,82 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const Params p) {
         for (int i = 0; i < 16; ++i)
           if (nb * 32 + 16 * (i / 8) + (i % 8) > lim) s[nb][i] = -INFINITY;
     }
-    // online softmax in base 2 (fa2/kernel.py:95-98)
+    // online softmax in base 2 (fa2/kernel.py:95-98), with a lazily moved reference max
     float mx = -INFINITY;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
-    mx = pair_max(mx);
-    const float m_new = fmaxf(m_i, mx * qk_scale);
-    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+    mx = pair_max(mx) * qk_scale;
+    const bool grow = mx > m_i + kRescaleTau;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? mx : m_i;
+      const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+      l_i *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+      m_i = m_new;
+    }
     float rs = 0.f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][i], qk_scale, -m_new));
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][i], qk_scale, -m_i));
         s[nb][i] = e;
         rs += e;
       }
-    l_i = l_i * alpha + rs;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) acc[db] *= alpha;
-    m_i = m_new;
-    // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
+    l_i += rs;
+    // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105); the V^T
+    // operands come from transposing LDS reads issued one MFMA ahead
+    u32x4 pb[BN / 16];
 #pragma unroll
     for (int t = 0; t < BN / 16; ++t) {
       const int nb = t >> 1, h = t & 1;
-      const u32x4 pb = {E::pack2(s[nb][8 * h + 0], s[nb][8 * h + 1]),
-                        E::pack2(s[nb][8 * h + 2], s[nb][8 * h + 3]),
-                        E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
-                        E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
+      pb[t] = u32x4{E::pack2(s[nb][8 * h + 0], s[nb][8 * h + 1]),
+                    E::pack2(s[nb][8 * h + 2], s[nb][8 * h + 3]),
+                    E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
+                    E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
+    }
+    auto v_operand = [&](int t, int db) {
+      u32x2 part[2];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        u32x2 part[2];
-#pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-          const int row = 16 * t + 8 * g + 4 * rr + vj;
-          const int chunk = (4 * db + 2 * vdh + (vsig >> 1)) ^ v_key<D>(row & 15);
-          part[rr] = lds_read_tr(v_lds_b + row * (D * 2) + chunk * 16 + (vsig & 1) * 8);
-        }
-        const u32x4 a = {part[0][0], part[0][1], part[1][0], part[1][1]};
-        acc[db] = E::mma(a, pb, acc[db]);
+      for (int rr = 0; rr < 2; ++rr) {
+        const int row = 16 * t + 8 * g + 4 * rr + vj;
+        const int chunk = (4 * db + 2 * vdh + (vsig >> 1)) ^ v_key<D>(row & 15);
+        part[rr] = lds_read_tr(vt + row * (D * 2) + chunk * 16 + (vsig & 1) * 8);
       }
+      return u32x4{part[0][0], part[0][1], part[1][0], part[1][1]};
+    };
+    constexpr int NPV = (BN / 16) * DB;
+    u32x4 va[2];
+    va[0] = v_operand(0, 0);
+#pragma unroll
+    for (int i = 0; i < NPV; ++i) {
+      if (i + 1 < NPV) va[(i + 1) & 1] = v_operand((i + 1) / DB, (i + 1) % DB);
+      acc[i % DB] = E::mma(va[i & 1], pb[i / DB], acc[i % DB]);
+    }
+#pragma unroll
+    for (int i = 0; i < NPV; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the next operand's two reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // this MFMA
     }
   };
 
-  // ---- main loop: prefetch tile j+1 into registers while tile j computes from LDS
-  if (0 < kv_end) gload(0);
-  for (int n0 = 0; n0 < kv_end; n0 += BN) {
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (n0 + BN < kv_end) gload(n0 + BN);
-    if (n0 + BN <= full_end)
-      step.template operator()<false>(n0);
-    else
-      step.template operator()<true>(n0);
+  // ---- main loop: tile j+1 streams HBM -> LDS while tile j is consumed
+  if (n_tiles_kv > 0) issue_tile(0, 0);
+  for (int j = 0; j < n_tiles_kv; ++j) {
+    const int n0 = j * BN;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile j have landed in LDS
+    __syncthreads();                // ... and every wave's; tile j-1's buffer is free
+    if (j + 1 < n_tiles_kv) issue_tile(n0 + BN, (j + 1) & 1);
+    step(n0, j & 1, n0 + BN > full_end);
   }
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
   const float l = pair_sum(l_i);
   if (row_ok) {
-    uint16_t* orow = p.o + b * p.sob + head * p.soh + (int64_t)pos * p.son;
+    uint16_t* orow = p.o + pr.b * p.sob + head * p.soh + (int64_t)pos * p.son;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll

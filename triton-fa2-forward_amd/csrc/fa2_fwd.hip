@@ -29,6 +29,8 @@ int fail(int code, const char* fmt, ...) {
 using fa2::Params;
 
 constexpr int kDims[4] = {16, 32, 64, 128};
+// 128 rows x stride x 2 bytes must stay below 2^31.
+constexpr int64_t kMaxRowStride = int64_t(1) << 22;
 
 // Per (dtype, head_dim) launchers, each compiled in its own translation unit.
 int launch(int dtype, int di, const Params& p, int waves, int block_n, bool causal, unsigned grid,
@@ -130,10 +132,14 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
       return fail(FA2_EALIGN, "the head_dim stride must be 1 (tensor %d has %lld)", t,
                   (long long)strides[t][3]);
     for (int j = 0; j < 3; ++j)
-      if (strides[t][j] % 8)
+      if (strides[t][j] % 8 || strides[t][j] < 0)
         return fail(FA2_EALIGN, "strides must be multiples of 8 elements (tensor %d dim %d: %lld)",
                     t, j, (long long)strides[t][j]);
   }
+  // K/V tiles are addressed with 32-bit byte offsets from the tile's first row.
+  if (k_stride[2] > kMaxRowStride || v_stride[2] > kMaxRowStride)
+    return fail(FA2_EINVAL, "k/v sequence stride above %lld elements is not supported",
+                (long long)kMaxRowStride);
 
   // block_m rows -> wave64s of 32 rows, rounded up to 1, 2, 4 or 8 (rows past block_m are
   // computed on zeros and dropped); block_n -> the next supported K/V tile width.

@@ -1,0 +1,52 @@
+"""One workload, a few launches: the process rocprofv3 profiles (counterpart of the reference's
+bench/profile_target.py).
+
+    python triton-fa2-forward_amd/profile_target.py --config C3 --launches 3
+    python triton-fa2-forward_amd/profile_target.py --config C3 --launches 3 --copy-mib 1024
+
+--copy-mib adds one plain device-to-device copy of that many MiB after the attention launches.
+Its FETCH_SIZE / WRITE_SIZE reading, against the bytes it is known to move, is the scale factor
+that turns the counters' KiB into bytes for the attention kernel.
+"""
+
+import argparse
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+sys.path.insert(0, os.path.dirname(HERE))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--config", default="C3")
+    ap.add_argument("--launches", type=int, default=3)
+    ap.add_argument("--copy-mib", type=int, default=0)
+    ap.add_argument("--block-m", type=int, default=None)
+    ap.add_argument("--block-n", type=int, default=None)
+    args = ap.parse_args()
+
+    import torch
+
+    import bench
+    from fa2.kernel import attention
+
+    q, k, v, causal = bench.make_inputs(args.config, "cuda")
+    print(f"profile_target: {bench.describe(args.config)}, {args.launches} launches", flush=True)
+    for _ in range(args.launches):
+        attention(q, k, v, causal=causal, block_m=args.block_m, block_n=args.block_n)
+    torch.cuda.synchronize()
+    if args.copy_mib:
+        n = args.copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"profile_target: copied {args.copy_mib} MiB ({n} bytes read, {n} written)", flush=True)
+    print("profile_target: done", flush=True)
+
+
+if __name__ == "__main__":
+    main()
