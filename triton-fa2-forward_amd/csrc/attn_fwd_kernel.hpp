@@ -262,29 +262,58 @@ void attn_fwd_kernel(const Params p) {
     koff[jj] = (uint32_t)(row * p.skn + (col ^ k_key<D>(pi_row(row & 31) & 15)) * 8) * 2u;
     voff[jj] = (uint32_t)(row * p.svn + (col ^ v_key<D>(row & 15)) * 8) * 2u;
   }
-  auto issue_tile = [&](int n0, int buf) {
+  auto rsrc_at = [&](const char* base, int64_t stride, int n0) {
     const int64_t rows_left = p.n_kv - n0;  // >= 1
-    const int64_t kbytes = ((rows_left - 1) * p.skn + D) * 2;
-    const int64_t vbytes = ((rows_left - 1) * p.svn + D) * 2;
-    const auto krs = make_rsrc(kbase + (int64_t)n0 * p.skn * 2, (uint32_t)min(kbytes, (int64_t)0x7fffffff));
-    const auto vrs = make_rsrc(vbase + (int64_t)n0 * p.svn * 2, (uint32_t)min(vbytes, (int64_t)0x7fffffff));
+    const int64_t bytes = ((rows_left - 1) * stride + D) * 2;
+    return make_rsrc(base + (int64_t)n0 * stride * 2, (uint32_t)min(bytes, (int64_t)0x7fffffff));
+  };
+  auto issue_k = [&](int n0, int buf) {
+    const auto rs = rsrc_at(kbase, p.skn, n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
       const int j = wave + jj * NW;
-      if (NI % NW == 0 || j < NI) {
-        load_lds16(krs, koff[jj], (void FA2_LDS*)&k_lds[buf][j * 64]);
-        load_lds16(vrs, voff[jj], (void FA2_LDS*)&v_lds[buf][j * 64]);
-      }
+      if (NI % NW == 0 || j < NI) load_lds16(rs, koff[jj], (void FA2_LDS*)&k_lds[buf][j * 64]);
+    }
+  };
+  auto issue_v = [&](int n0, int buf) {
+    const auto rs = rsrc_at(vbase, p.svn, n0);
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) {
+      const int j = wave + jj * NW;
+      if (NI % NW == 0 || j < NI) load_lds16(rs, voff[jj], (void FA2_LDS*)&v_lds[buf][j * 64]);
     }
   };
 
-  // per-lane LDS offsets that do not change across tiles
+  // ---- LDS operand reads
   const int kk = k_key<D>(c & 15);
   const int vs = lane & 15;          // role inside the 16-lane transpose group
   const int vj = vs >> 2;            // key row within the 4-row block it addresses
   const int vq = vs & 3;
   const int vsig = ((vq & 1) << 1) | ((vq & 2) >> 1);
   const int vdh = (D == 16) ? 0 : ((lane >> 4) & 1);
+  // A operand of S^T: 32 keys (rows pi(c) of key block nb) x 16 dims (k-step ks)
+  auto k_operand = [&](int buf, int ks, int nb) {
+    const u32x4 FA2_LDS* kt = (const u32x4 FA2_LDS*)k_lds[buf];
+    return kt[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + g) ^ kk)];
+  };
+  // The same read, volatile: used before the loop so that the compiler cannot merge it with
+  // the in-loop prefetch into one load at the top of the loop (which would expose its latency).
+  auto k_operand_v = [&](int buf, int ks, int nb) {
+    const volatile u32x4 FA2_LDS* kt = (const volatile u32x4 FA2_LDS*)k_lds[buf];
+    return kt[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + g) ^ kk)];
+  };
+  // A operand of O^T: 32 dims (block db) x 16 keys (k-step t), two transposing reads
+  auto v_operand = [&](int buf, int t, int db) {
+    const char FA2_LDS* vt = (const char FA2_LDS*)v_lds[buf];
+    u32x2 part[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int row = 16 * t + 8 * g + 4 * rr + vj;
+      const int chunk = (4 * db + 2 * vdh + (vsig >> 1)) ^ v_key<D>(row & 15);
+      part[rr] = lds_read_tr(vt + row * (D * 2) + chunk * 16 + (vsig & 1) * 8);
+    }
+    return u32x4{part[0][0], part[0][1], part[1][0], part[1][1]};
+  };
 
   // ---- online-softmax state (fa2/kernel.py:146-148); l is a per-lane partial sum
   float m_i = -INFINITY;
@@ -292,38 +321,69 @@ void attn_fwd_kernel(const Params p) {
   f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
-
   const float qk_scale = p.qk_scale;
 
-  auto step = [&](int n0, int buf, bool masked) {
-    const u32x4 FA2_LDS* kt = (const u32x4 FA2_LDS*)k_lds[buf];
-    const char FA2_LDS* vt = (const char FA2_LDS*)v_lds[buf];
-    // S^T = K Q^T  (fa2/kernel.py:75-79); K operands are read one k-step ahead
+  // ---- main loop. Per tile j, one barrier, placed between the two products:
+  //   S_j = K_j Q^T                      K_j's operands partly read during PV_{j-1}
+  //   wait + barrier                     V_j and K_{j+1} have landed; every wave is past S_j
+  //   issue K_{j+2} -> K buffer of K_j, V_{j+1} -> V buffer of V_{j-1}
+  //   read the first V_j operands, then mask + softmax_j while they arrive
+  //   O += V_j P_j, with V_j operands read LA_V MFMAs ahead and K_{j+1}'s first operands
+  //   read in between, so every LDS read has MFMA time to land in.
+  constexpr int LA_S = KS < 4 ? KS : 4;        // k-steps of K operands read ahead
+  constexpr int NPV = (BN / 16) * DB;          // MFMAs of the PV product
+  constexpr int LA_V = NPV < 4 ? NPV : 4;      // PV MFMAs whose V operands are read ahead
+  constexpr int NKP = LA_S * NB;               // K operand reads prefetched during PV
+  u32x4 kop[LA_S][NB];
+  if (n_tiles_kv > 0) {
+    issue_k(0, 0);
+    issue_v(0, 0);
+    if (n_tiles_kv > 1) issue_k(BN, 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < LA_S; ++ks)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand_v(0, ks, nb);
+  }
+  for (int j = 0; j < n_tiles_kv; ++j) {
+    const int n0 = j * BN;
+    const int buf = j & 1;
+
+    // S^T = K Q^T  (fa2/kernel.py:75-79)
     f32x16 s[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) s[nb] = f32x16{};
-    u32x4 ka[2][NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) ka[0][nb] = kt[(nb * 32 + pi_row(c)) * CPR + (g ^ kk)];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) {
+      const int slot = ks % LA_S;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          ka[(ks + 1) & 1][nb] = kt[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + 2 + g) ^ kk)];
+      for (int nb = 0; nb < NB; ++nb) s[nb] = E::mma(kop[slot][nb], qreg[ks], s[nb]);
+      if (ks + LA_S < KS) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) kop[slot][nb] = k_operand(buf, ks + LA_S, nb);
       }
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) s[nb] = E::mma(ka[ks & 1][nb], qreg[ks], s[nb]);
     }
+    // keep the K reads LA_S k-steps ahead of the MFMAs that consume them
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);  // DS reads of the next k-step
-      __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);  // MFMAs of this k-step
+      __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
+      if (ks + LA_S < KS) __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
     }
+
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of V_j and K_{j+1} have landed
+    __syncthreads();                // ... every wave's; and every wave is done with K_j
+    if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, buf);
+    if (j + 1 < n_tiles_kv) issue_v(n0 + BN, buf ^ 1);
+
+    u32x4 va[LA_V];
+#pragma unroll
+    for (int i = 0; i < LA_V; ++i) va[i] = v_operand(buf, i / DB, i % DB);
+
     // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos.
     // `masked` is uniform over the workgroup; one copy of the tile code serves both cases
     // so the accumulators keep one register assignment across the loop.
-    if (masked) {
+    if (n0 + BN > full_end) {
       const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -357,8 +417,8 @@ void attn_fwd_kernel(const Params p) {
         rs += e;
       }
     l_i += rs;
-    // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105); the V^T
-    // operands come from transposing LDS reads issued one MFMA ahead
+
+    // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
     u32x4 pb[BN / 16];
 #pragma unroll
     for (int t = 0; t < BN / 16; ++t) {
@@ -368,39 +428,23 @@ void attn_fwd_kernel(const Params p) {
                     E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
                     E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
     }
-    auto v_operand = [&](int t, int db) {
-      u32x2 part[2];
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        const int row = 16 * t + 8 * g + 4 * rr + vj;
-        const int chunk = (4 * db + 2 * vdh + (vsig >> 1)) ^ v_key<D>(row & 15);
-        part[rr] = lds_read_tr(vt + row * (D * 2) + chunk * 16 + (vsig & 1) * 8);
-      }
-      return u32x4{part[0][0], part[0][1], part[1][0], part[1][1]};
-    };
-    constexpr int NPV = (BN / 16) * DB;
-    u32x4 va[2];
-    va[0] = v_operand(0, 0);
 #pragma unroll
     for (int i = 0; i < NPV; ++i) {
-      if (i + 1 < NPV) va[(i + 1) & 1] = v_operand((i + 1) / DB, (i + 1) % DB);
-      acc[i % DB] = E::mma(va[i & 1], pb[i / DB], acc[i % DB]);
+      acc[i % DB] = E::mma(va[i % LA_V], pb[i / DB], acc[i % DB]);
+      if (i + LA_V < NPV) va[i % LA_V] = v_operand(buf, (i + LA_V) / DB, (i + LA_V) % DB);
+      // K_{j+1}'s first operands (a harmless stale read after the last tile)
+#pragma unroll
+      for (int r = i * NKP / NPV; r < (i + 1) * NKP / NPV; ++r)
+        kop[r / NB][r % NB] = k_operand(buf ^ 1, r / NB, r % NB);
     }
+    // MFMA i, then the reads it makes room for (V operands LA_V ahead, K prefetch)
 #pragma unroll
     for (int i = 0; i < NPV; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the next operand's two reads
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // this MFMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      const int nreads = (i + LA_V < NPV ? 2 : 0) + ((i + 1) * NKP / NPV - i * NKP / NPV);
+#pragma unroll
+      for (int k = 0; k < nreads; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-  };
-
-  // ---- main loop: tile j+1 streams HBM -> LDS while tile j is consumed
-  if (n_tiles_kv > 0) issue_tile(0, 0);
-  for (int j = 0; j < n_tiles_kv; ++j) {
-    const int n0 = j * BN;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile j have landed in LDS
-    __syncthreads();                // ... and every wave's; tile j-1's buffer is free
-    if (j + 1 < n_tiles_kv) issue_tile(n0 + BN, (j + 1) & 1);
-    step(n0, j & 1, n0 + BN > full_end);
   }
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
