@@ -17,7 +17,10 @@ Protocol (the reference's, bench/bench.py:51-92, restated for ROCm):
   * a second pass follows the reference's flush protocol exactly: a 1 GiB fill (larger than
     L2 + the 256 MB Infinity Cache) before every iteration, median of per-iteration events;
   * cpu_baseline: the oracle's blocked_attention (the reference's CPU path, fa2/reference.py:
-    35-82, restated) timed on this host on one (batch, head) of the workload, scaled by B*H_q.
+    35-82, restated) timed on this host, one thread, on whole (batch, head) pairs of the
+    workload until at least 10 s of CPU work, reported as its TFLOP/s;
+  * roofline.traffic: HBM bytes per launch from the committed rocprofv3 counter summary
+    (profiles/hbm_traffic.json), next to the algorithmic minimum (q, k, v read, out written).
 
 Prints ONE JSON line. --gpus N with N > 1 exits: this build is one GPU per box.
 """
@@ -145,38 +148,57 @@ def flushed_median(fn, iters):
     return {"median_ms": med, "p25_ms": q1, "p75_ms": q3}
 
 
-def cpu_baseline(name, q, k, v, causal):
-    """The reference's CPU path (blocked_attention, restated in oracle/) on one (b, h) of the
-    workload, single thread, on CPU copies of the same inputs; scaled to the whole job."""
+def cpu_baseline(name, q, k, v, causal, min_seconds=10.0):
+    """The reference's CPU path (blocked_attention, restated in oracle/) on whole (b, h) pairs
+    of the workload, single thread, on CPU copies of the same inputs, until at least
+    `min_seconds` of CPU work; scaled to the whole job by per-head work (identical per head)."""
     import torch
 
     from oracle import reference as ref
 
     B, H_q, N, D = q.shape
     group = H_q // k.shape[1]
-    qs = q[:1, :1].cpu()
-    ks, vs = k[:1, :1].cpu(), v[:1, :1].cpu()
     threads = torch.get_num_threads()
     torch.set_num_threads(1)
+    done, dt = 0, 0.0
     try:
-        t0 = time.perf_counter()
-        ref.blocked_attention(qs, ks, vs, causal=causal)
-        dt = time.perf_counter() - t0
+        while dt < min_seconds and done < B * H_q:
+            b, h = divmod(done, H_q)
+            qs = q[b:b + 1, h:h + 1].cpu()
+            ks = k[b:b + 1, h // group:h // group + 1].cpu()
+            vs = v[b:b + 1, h // group:h // group + 1].cpu()
+            t0 = time.perf_counter()
+            ref.blocked_attention(qs, ks, vs, causal=causal)
+            dt += time.perf_counter() - t0
+            done += 1
     finally:
         torch.set_num_threads(threads)
-    sample_flops = attn_flops(1, 1, N, k.shape[2], D, causal)
+    sample_flops = done * attn_flops(1, 1, N, k.shape[2], D, causal)
     return {
         "value": sample_flops / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": 1,
         "kind": "port",
         "sample": (f"oracle.blocked_attention (fa2/reference.py:35-82 restated; block 32x16, fp32 "
-                   f"state) on 1 of {B * H_q} (batch, head) pairs of {name} (group {group}), "
+                   f"state) on {done} of {B * H_q} (batch, head) pairs of {name} (group {group}), "
                    f"{dt:.1f} s on 1 thread of {os.cpu_count()} host CPUs; per-head work is "
                    f"identical, so the rate holds for the whole job"),
         "seconds": dt,
-        "est_full_job_s": dt * B * H_q,
+        "est_full_job_s": dt * B * H_q / done,
     }
+
+
+def measured_traffic(name):
+    """HBM bytes per launch for this workload from the committed rocprofv3 counter summary
+    (profiles/hbm_traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what
+    the counter reads for a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["configs"][name]
+        return {"bytes": entry["bytes"], "source": f"profiles/hbm_traffic.json ({entry['kernel_build']})"}
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def gpu_env():
@@ -214,6 +236,8 @@ def run(name, steps, warmup, with_cpu, flush_iters):
     q1, med, q3 = statistics.quantiles(per, n=4, method="inclusive") if len(per) > 1 else (per[0],) * 3
     value = flops * steps / (total_ms * 1e-3) / 1e12
     achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
+    traffic = measured_traffic(name)
+    min_bytes = sum(t.numel() * t.element_size() for t in (q, k, v)) + out.numel() * out.element_size()
     res = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -232,7 +256,10 @@ def run(name, steps, warmup, with_cpu, flush_iters):
                    "flops_rule": "4*B*H_q*pairs*D, causal pairs N(N+1)/2 (bench/bench.py:83-87)"},
         "pct_of_peak": round(100 * value / PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(PEAK_TFLOPS, 1),
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
+                     "algorithmic_bytes": min_bytes,
                      "kernel": "fa2::attn_fwd_kernel", "avg_kernel_ms": round(avg_kernel_ms, 5)},
         "median_ms": round(med, 5), "p25_ms": round(q1, 5), "p75_ms": round(q3, 5),
         "host_wall_ms": round(wall_ms, 3),
