@@ -193,3 +193,36 @@ def test_oracle_on_gpu_matches_oracle_on_cpu():
     cpu = truth(qs, ks, vs, causal, torch.float64)
     gpu = truth(qs.cuda(), ks.cuda(), vs.cuda(), causal, torch.float32).cpu()
     assert (gpu.double() - cpu).abs().max().item() < 1e-5
+
+
+# ------------------------------------------------------------------------------------------
+# the 64-rows-per-wave kernel (block_m 128 / 256 over 32-key tiles, head_dim 64 / 128)
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("block_m", [128, 256])
+@pytest.mark.parametrize("N", [1, 33, 100, 1000, 2048])
+def test_kernel_r64_family(dtype, causal, D, block_m, N):
+    q, k, v = make_qkv(BATCH, 16, 4, N, N, D, dtype)
+    check_against_oracle(q, k, v, causal, block_m=block_m, block_n=32)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_kernel_r64_pack_and_lengths(causal):
+    attention = _attention()
+    q, k, v = make_qkv(BATCH, 32, 8, 1000, 1000, 128, torch.bfloat16)
+    packed = attention(q, k, v, causal=causal, block_m=128, block_n=32, pack_gqa=True)
+    unpacked = attention(q, k, v, causal=causal, block_m=128, block_n=32, pack_gqa=False)
+    assert torch.equal(packed, unpacked)
+    check_against_oracle(q, k, v, causal, ours=packed)
+    if not causal:
+        q2, k2, v2 = make_qkv(BATCH, 8, 2, 77, 300, 64, torch.float16)
+        check_against_oracle(q2, k2, v2, False, block_m=256, block_n=32)
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5"])
+def test_baseline_config_r64(name):
+    q, k, v, causal = ref.baseline_inputs(name, device="cuda")
+    check_against_oracle(q, k, v, causal, precision=torch.float32, block_m=256, block_n=32)

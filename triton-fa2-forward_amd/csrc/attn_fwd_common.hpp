@@ -1,0 +1,179 @@
+// attn_fwd_common.hpp - types and device helpers shared by the forward kernels:
+// the MFMA / conversion traits per element type, the LDS swizzle keys, lane-pair reductions,
+// the transposing LDS read, the HBM -> LDS buffer loads and the program renumbering.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_fwd_params.hpp"
+
+namespace fa2 {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+#define FA2_LDS __attribute__((address_space(3)))
+#define FA2_GLOBAL __attribute__((address_space(1)))
+
+// Number of XCDs (each with its own L2) that the hardware deals workgroups to round-robin.
+constexpr int kXcds = 8;
+// Lazy-rescale threshold in exp2 units: the reference max lags the true max by at most this.
+constexpr float kRescaleTau = 8.0f;
+
+// ---------------------------------------------------------------------------------
+// element type traits: the MFMA and the fp32 -> 16-bit pair conversion (RNE)
+// ---------------------------------------------------------------------------------
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<0> {  // fp16
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    f16x2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+template <>
+struct Elem<1> {  // bf16
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+// ---------------------------------------------------------------------------------
+// index helpers
+// ---------------------------------------------------------------------------------
+
+// Swap bits 2 and 3 of a row index inside a 32-row block (an involution).
+__device__ __forceinline__ constexpr int pi_row(int x) {
+  return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1);
+}
+
+// XOR key of the K tile's 16-byte chunks. u = pi_row(row % 32) % 16, i.e. the lane index
+// (mod 16) that reads this row. Chosen (exhaustive search over linear keys) so that the
+// b128 A-operand reads are conflict-free for 32- and 64-bank LDS models.
+template <int D>
+__device__ __forceinline__ int k_key(int u) {
+  if constexpr (D == 128) {
+    return u & 15;
+  } else if constexpr (D == 64) {
+    return ((u >> 1) & 1) | (((u >> 2) & 1) << 1) | (((u ^ (u >> 3)) & 1) << 2);
+  } else if constexpr (D == 32) {
+    return ((u >> 2) & 1) | ((((u >> 1) ^ (u >> 3)) & 1) << 1);
+  } else {
+    return (u >> 2) & 1;
+  }
+}
+
+// XOR key of the V tile's 16-byte chunks, a function of the key row (mod 16); makes the
+// ds_read_b64_tr_b16 reads conflict-free for 32- and 64-bank LDS models.
+template <int D>
+__device__ __forceinline__ int v_key(int row) {
+  if constexpr (D == 128) {
+    return ((row & 1) << 1) | ((row & 2) << 1) | ((row & 1) << 3);
+  } else if constexpr (D == 64) {
+    return ((row & 1) << 1) | ((row & 2) << 1);
+  } else if constexpr (D == 32) {
+    return row & 2;
+  } else {
+    return 0;
+  }
+}
+
+// max / sum of a value over the lane pair (l, l^32)
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ u32x2 lds_read_tr(const char FA2_LDS* p) {
+  i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 FA2_LDS*)p);
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// A raw buffer resource (gfx9 layout) over [base, base + bytes): loads past `bytes` return
+// zeros. Built from wave-uniform values, so it lives in SGPRs.
+__device__ __forceinline__ u32x4 make_desc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  auto uniform = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
+  return u32x4{uniform((uint32_t)a), uniform((uint32_t)(a >> 32) & 0xffffu), uniform(bytes),
+               0x00020000u};
+}
+
+// LDS byte address of a __shared__ object, as a wave-uniform value.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const FA2_LDS void*)p);
+}
+
+// 16 bytes HBM -> LDS without VGPRs: lane l of the wave writes lds_base + 16 * l
+// (buffer_load_dwordx4 ... lds, LDS destination in M0). Issued as inline asm on purpose: the
+// compiler's own LDS-DMA intrinsic makes it wait for every DMA in flight before the next LDS
+// read of any buffer (it cannot prove the double buffers apart), which serialises the
+// prefetch. Callers wait with wait_vmcnt<N>() before a barrier instead. M0 is used by nothing
+// else in these kernels.
+__device__ __forceinline__ void load_lds16(u32x4 desc, uint32_t voffset, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(desc), "s"(lds_base)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N), leaving the other counters alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// The workgroup -> (q tile, batch, first query head) decomposition. Workgroups are dealt to
+// the XCDs round-robin; block b runs on XCD b % 8. Renumber so that each XCD receives a
+// contiguous range of "virtual" programs, ordered (batch, kv head) outermost, then q tile
+// (heaviest causal tile first), then the query-head groups sharing that KV head: an XCD's L2
+// then holds the K/V of the heads it is working on.
+struct Program {
+  int tile, b, hq0, hkv;
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ Program program_of(const Params& p, int block) {
+  const int total = p.n_tiles * p.n_bh;
+  const int q = total / kXcds, rem = total % kXcds;
+  const int xcd = block % kXcds, slot = block / kXcds;
+  const int v = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + slot;
+  const int progs_per_kv = p.group / p.pack;  // programs sharing one KV head per q tile
+  const int per_kv = p.n_tiles * progs_per_kv;
+  const int kv_index = v / per_kv;            // b * h_kv + hkv
+  const int r = v - kv_index * per_kv;
+  const int t = r / progs_per_kv;
+  const int h_in = r - t * progs_per_kv;
+  const int h_kv = p.h_q / p.group;
+  Program pr;
+  pr.tile = CAUSAL ? p.n_tiles - 1 - t : t;
+  pr.b = kv_index / h_kv;
+  pr.hkv = kv_index - pr.b * h_kv;
+  pr.hq0 = pr.hkv * p.group + h_in * p.pack;
+  return pr;
+}
+
+}  // namespace fa2

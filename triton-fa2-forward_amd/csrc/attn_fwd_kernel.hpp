@@ -37,155 +37,9 @@
 //     heaviest causal tiles first.
 #pragma once
 
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-
-#include "attn_fwd_params.hpp"
+#include "attn_fwd_common.hpp"
 
 namespace fa2 {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-
-#define FA2_LDS __attribute__((address_space(3)))
-#define FA2_GLOBAL __attribute__((address_space(1)))
-
-// Number of XCDs (each with its own L2) that the hardware deals workgroups to round-robin.
-constexpr int kXcds = 8;
-// Lazy-rescale threshold in exp2 units: the reference max lags the true max by at most this.
-constexpr float kRescaleTau = 8.0f;
-
-// ---------------------------------------------------------------------------------
-// element type traits: the MFMA and the fp32 -> 16-bit pair conversion (RNE)
-// ---------------------------------------------------------------------------------
-template <int DT>
-struct Elem;
-
-template <>
-struct Elem<0> {  // fp16
-  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    f16x2 v = {(_Float16)lo, (_Float16)hi};
-    return __builtin_bit_cast(uint32_t, v);
-  }
-};
-
-template <>
-struct Elem<1> {  // bf16
-  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    bf16x2 v = {(__bf16)lo, (__bf16)hi};
-    return __builtin_bit_cast(uint32_t, v);
-  }
-};
-
-// ---------------------------------------------------------------------------------
-// index helpers
-// ---------------------------------------------------------------------------------
-
-// Swap bits 2 and 3 of a row index inside a 32-row block (an involution).
-__device__ __forceinline__ constexpr int pi_row(int x) {
-  return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1);
-}
-
-// XOR key of the K tile's 16-byte chunks. u = pi_row(row % 32) % 16, i.e. the lane index
-// (mod 16) that reads this row. Chosen (exhaustive search over linear keys) so that the
-// b128 A-operand reads are conflict-free for 32- and 64-bank LDS models.
-template <int D>
-__device__ __forceinline__ int k_key(int u) {
-  if constexpr (D == 128) {
-    return u & 15;
-  } else if constexpr (D == 64) {
-    return ((u >> 1) & 1) | (((u >> 2) & 1) << 1) | (((u ^ (u >> 3)) & 1) << 2);
-  } else if constexpr (D == 32) {
-    return ((u >> 2) & 1) | ((((u >> 1) ^ (u >> 3)) & 1) << 1);
-  } else {
-    return (u >> 2) & 1;
-  }
-}
-
-// XOR key of the V tile's 16-byte chunks, a function of the key row (mod 16); makes the
-// ds_read_b64_tr_b16 reads conflict-free for 32- and 64-bank LDS models.
-template <int D>
-__device__ __forceinline__ int v_key(int row) {
-  if constexpr (D == 128) {
-    return ((row & 1) << 1) | ((row & 2) << 1) | ((row & 1) << 3);
-  } else if constexpr (D == 64) {
-    return ((row & 1) << 1) | ((row & 2) << 1);
-  } else if constexpr (D == 32) {
-    return row & 2;
-  } else {
-    return 0;
-  }
-}
-
-// max / sum of a value over the lane pair (l, l^32)
-__device__ __forceinline__ float pair_max(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float pair_sum(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-__device__ __forceinline__ u32x2 lds_read_tr(const char FA2_LDS* p) {
-  i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 FA2_LDS*)p);
-  return __builtin_bit_cast(u32x2, v);
-}
-
-// A raw buffer resource over [base, base + bytes): loads past `bytes` return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-// 16 bytes HBM -> LDS without VGPRs: lane l of the wave writes lds_base + 16 * l.
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
-                                           void FA2_LDS* lds_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_base, 16, voffset, 0, 0, 0);
-}
-
-// The workgroup -> (q tile, batch, first query head) decomposition. Workgroups are dealt to
-// the XCDs round-robin; block b runs on XCD b % 8. Renumber so that each XCD receives a
-// contiguous range of "virtual" programs, ordered (batch, kv head) outermost, then q tile
-// (heaviest causal tile first), then the query-head groups sharing that KV head: an XCD's L2
-// then holds the K/V of the heads it is working on.
-struct Program {
-  int tile, b, hq0, hkv;
-};
-
-template <bool CAUSAL>
-__device__ __forceinline__ Program program_of(const Params& p, int block) {
-  const int total = p.n_tiles * p.n_bh;
-  const int q = total / kXcds, rem = total % kXcds;
-  const int xcd = block % kXcds, slot = block / kXcds;
-  const int v = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + slot;
-  const int progs_per_kv = p.group / p.pack;  // programs sharing one KV head per q tile
-  const int per_kv = p.n_tiles * progs_per_kv;
-  const int kv_index = v / per_kv;            // b * h_kv + hkv
-  const int r = v - kv_index * per_kv;
-  const int t = r / progs_per_kv;
-  const int h_in = r - t * progs_per_kv;
-  const int h_kv = p.h_q / p.group;
-  Program pr;
-  pr.tile = CAUSAL ? p.n_tiles - 1 - t : t;
-  pr.b = kv_index / h_kv;
-  pr.hkv = kv_index - pr.b * h_kv;
-  pr.hq0 = pr.hkv * p.group + h_in * p.pack;
-  return pr;
-}
 
 // ---------------------------------------------------------------------------------
 // the kernel
@@ -265,14 +119,14 @@ void attn_fwd_kernel(const Params p) {
   auto rsrc_at = [&](const char* base, int64_t stride, int n0) {
     const int64_t rows_left = p.n_kv - n0;  // >= 1
     const int64_t bytes = ((rows_left - 1) * stride + D) * 2;
-    return make_rsrc(base + (int64_t)n0 * stride * 2, (uint32_t)min(bytes, (int64_t)0x7fffffff));
+    return make_desc(base + (int64_t)n0 * stride * 2, (uint32_t)min(bytes, (int64_t)0x7fffffff));
   };
   auto issue_k = [&](int n0, int buf) {
     const auto rs = rsrc_at(kbase, p.skn, n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
       const int j = wave + jj * NW;
-      if (NI % NW == 0 || j < NI) load_lds16(rs, koff[jj], (void FA2_LDS*)&k_lds[buf][j * 64]);
+      if (NI % NW == 0 || j < NI) load_lds16(rs, koff[jj], lds_addr(&k_lds[buf][j * 64]));
     }
   };
   auto issue_v = [&](int n0, int buf) {
@@ -280,7 +134,7 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
       const int j = wave + jj * NW;
-      if (NI % NW == 0 || j < NI) load_lds16(rs, voff[jj], (void FA2_LDS*)&v_lds[buf][j * 64]);
+      if (NI % NW == 0 || j < NI) load_lds16(rs, voff[jj], lds_addr(&v_lds[buf][j * 64]));
     }
   };
 
@@ -339,7 +193,7 @@ void attn_fwd_kernel(const Params p) {
     issue_k(0, 0);
     issue_v(0, 0);
     if (n_tiles_kv > 1) issue_k(BN, 1);
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_vmcnt<0>();
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < LA_S; ++ks)
@@ -371,7 +225,7 @@ void attn_fwd_kernel(const Params p) {
       if (ks + LA_S < KS) __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
     }
 
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of V_j and K_{j+1} have landed
+    wait_vmcnt<0>();  // this wave's loads of V_j and K_{j+1} have landed
     __syncthreads();                // ... every wave's; and every wave is done with K_j
     if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, buf);
     if (j + 1 < n_tiles_kv) issue_v(n0 + BN, buf ^ 1);
