@@ -25,7 +25,7 @@
 //     4-key x 16-dim block and every lane receives 4 consecutive keys of one dim.
 //   * O^T accumulates in 32x32 blocks whose lane l holds column l%32 = the lane's own
 //     query row, so the per-row rescale by alpha is a lane-local multiply.
-//   * K/V tiles go HBM -> LDS directly (global_load_lds_dwordx4, no VGPR staging) into a
+//   * K/V tiles go HBM -> LDS directly (buffer_load_dwordx4 ... lds, no VGPR staging) into a
 //     double buffer: tile j+1 is in flight while tile j is consumed; one barrier per tile.
 //   * LDS layouts are XOR-swizzled at 16-byte granularity so that both the b128 reads
 //     of K and the transposing b64 reads of V are free of bank conflicts; the swizzle is
@@ -60,7 +60,7 @@ void attn_fwd_kernel(const Params p) {
   __shared__ u32x4 v_lds[2][TCH];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS addresses stay scalar
   const int lane = tid & 63;
   const int c = lane & 31;
   const int g = lane >> 5;
@@ -145,28 +145,40 @@ void attn_fwd_kernel(const Params p) {
   const int vq = vs & 3;
   const int vsig = ((vq & 1) << 1) | ((vq & 2) >> 1);
   const int vdh = (D == 16) ? 0 : ((lane >> 4) & 1);
+  // Per-lane byte offsets of the operand reads inside a tile, computed once. The XOR keys make
+  // them lane-dependent only through the k-step (K) or the row half and dim block (V); the key
+  // block nb (K) and the key step t (V) only add a constant, which the ds_read's immediate
+  // offset absorbs, so a tile's reads need one VALU add per offset for the buffer base.
+  uint32_t koffs[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    koffs[ks] = (uint32_t)((pi_row(c) * CPR + ((2 * ks + g) ^ kk)) * 16);
+  uint32_t voffs[2][DB];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int row = 8 * g + 4 * rr + vj;  // row & 15 of every key step's row 16 t + row
+      const int chunk = (4 * db + 2 * vdh + (vsig >> 1)) ^ v_key<D>(row);
+      voffs[rr][db] = (uint32_t)(row * (D * 2) + chunk * 16 + (vsig & 1) * 8);
+    }
   // A operand of S^T: 32 keys (rows pi(c) of key block nb) x 16 dims (k-step ks)
   auto k_operand = [&](int buf, int ks, int nb) {
-    const u32x4 FA2_LDS* kt = (const u32x4 FA2_LDS*)k_lds[buf];
-    return kt[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + g) ^ kk)];
+    const char FA2_LDS* kt = (const char FA2_LDS*)k_lds[buf] + koffs[ks];
+    return *(const u32x4 FA2_LDS*)(kt + nb * 32 * CPR * 16);
   };
   // The same read, volatile: used before the loop so that the compiler cannot merge it with
   // the in-loop prefetch into one load at the top of the loop (which would expose its latency).
   auto k_operand_v = [&](int buf, int ks, int nb) {
-    const volatile u32x4 FA2_LDS* kt = (const volatile u32x4 FA2_LDS*)k_lds[buf];
-    return kt[(nb * 32 + pi_row(c)) * CPR + ((2 * ks + g) ^ kk)];
+    const char FA2_LDS* kt = (const char FA2_LDS*)k_lds[buf] + koffs[ks];
+    return *(const volatile u32x4 FA2_LDS*)(kt + nb * 32 * CPR * 16);
   };
   // A operand of O^T: 32 dims (block db) x 16 keys (k-step t), two transposing reads
   auto v_operand = [&](int buf, int t, int db) {
     const char FA2_LDS* vt = (const char FA2_LDS*)v_lds[buf];
-    u32x2 part[2];
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int row = 16 * t + 8 * g + 4 * rr + vj;
-      const int chunk = (4 * db + 2 * vdh + (vsig >> 1)) ^ v_key<D>(row & 15);
-      part[rr] = lds_read_tr(vt + row * (D * 2) + chunk * 16 + (vsig & 1) * 8);
-    }
-    return u32x4{part[0][0], part[0][1], part[1][0], part[1][1]};
+    const u32x2 lo = lds_read_tr(vt + voffs[0][db] + t * 16 * D * 2);
+    const u32x2 hi = lds_read_tr(vt + voffs[1][db] + t * 16 * D * 2);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
 
   // ---- online-softmax state (fa2/kernel.py:146-148); l is a per-lane partial sum
@@ -204,7 +216,11 @@ void attn_fwd_kernel(const Params p) {
     const int n0 = j * BN;
     const int buf = j & 1;
 
-    // S^T = K Q^T  (fa2/kernel.py:75-79)
+    // S^T = K Q^T  (fa2/kernel.py:75-79). The two products run at raised wave priority and
+    // the softmax at the base one, so that when the two waves of a SIMD meet, the one with
+    // matrix work issues first and the other's softmax fills the issue slots the MFMAs leave
+    // (3% on MI355X over equal priorities; raising it for only one of the products gains nothing).
+    __builtin_amdgcn_s_setprio(1);
     f32x16 s[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) s[nb] = f32x16{};
@@ -225,6 +241,7 @@ void attn_fwd_kernel(const Params p) {
       if (ks + LA_S < KS) __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
     }
 
+    __builtin_amdgcn_s_setprio(0);
     wait_vmcnt<0>();  // this wave's loads of V_j and K_{j+1} have landed
     __syncthreads();                // ... every wave's; and every wave is done with K_j
     if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, buf);
@@ -282,6 +299,7 @@ void attn_fwd_kernel(const Params p) {
                     E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
                     E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
     }
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int i = 0; i < NPV; ++i) {
       acc[i % DB] = E::mma(va[i % LA_V], pb[i / DB], acc[i % DB]);
@@ -300,6 +318,8 @@ void attn_fwd_kernel(const Params p) {
       for (int k = 0; k < nreads; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
   }
+
+  __builtin_amdgcn_s_setprio(0);
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
   const float l = pair_sum(l_i);

@@ -57,7 +57,7 @@ void attn_fwd_pipe_kernel(const Params p) {
   __shared__ u32x4 v_lds[2][TCH];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS addresses stay scalar
   const int lane = tid & 63;
   const int c = lane & 31;
   const int g = lane >> 5;
