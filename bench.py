@@ -2,6 +2,7 @@
 """Headline benchmark: attention forward TFLOP/s and % of the dense bf16 MFMA peak, one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config C3] [--all] [--no-cpu-baseline]
+    python bench.py --pack-short     # the reference's few-queries table (K/V read rate)
 
 Workload: BASELINE.json's target config C3 (bf16 causal GQA, B=1, H_q=32, H_kv=8, N=8192,
 D=128), the shape the reference's own bench defaults to (bench/bench.py:228-235) and the one
@@ -306,6 +307,60 @@ def run(name, steps, warmup, with_cpu, flush_iters):
     return res
 
 
+# The reference's few-queries table (README.md:282-301, bench/gpu_session.sh:27-28): batch 16,
+# H_q 32, H_kv 8, N_kv 4096, D 128, non-causal fp16; its default path's median us on H100
+# (packed where should_pack_gqa packs: N_q <= 64; unpacked above).
+PACK_SHORT = {"B": 16, "H_q": 32, "H_kv": 8, "N_kv": 4096, "D": 128}
+PACK_SHORT_H100_US = {1: 106.5, 16: 105.5, 32: 107.6, 64: 151.2, 128: 307.9, 256: 642.5}
+HBM_PEAK_GBS = 8000.0
+
+
+def run_pack_short(n_q, steps, warmup):
+    """One line of the few-queries regime: median kernel time and the K/V read rate
+    (bench/bench.py:90-92: bytes of K and V over the time, the bound when N_q is small)."""
+    import torch
+
+    from fa2 import _lib
+    from fa2.kernel import _cu_count, attention, should_pack_gqa
+
+    c = PACK_SHORT
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q = torch.randn(c["B"], c["H_q"], n_q, c["D"], generator=g).half().cuda()
+    k = torch.randn(c["B"], c["H_kv"], c["N_kv"], c["D"], generator=g).half().cuda()
+    v = torch.randn(c["B"], c["H_kv"], c["N_kv"], c["D"], generator=g).half().cuda()
+    fn = lambda: attention(q, k, v, causal=False)  # noqa: E731
+    out = fn()
+    torch.cuda.synchronize()
+    err, backend = correctness_gate(out, q, k, v, False)
+    if err is not None and not (math.isfinite(err) and err <= 2e-2):
+        raise SystemExit(f"correctness gate failed on pack-short N_q={n_q}: max-abs vs SDPA {err:.3e}")
+    settle = settle_clocks(fn)
+    per, total_ms, _ = time_steps(fn, steps, warmup)
+    med = statistics.median(per)
+    kv = 2 * k.numel() * k.element_size()
+    rate_gbs = kv / (med * 1e-3) / 1e9
+    splits = _lib.num_splits(c["B"], c["H_q"], c["H_kv"], n_q, c["N_kv"], c["D"], False, 128, 64,
+                             _cu_count(q.device))
+    return {
+        "metric": "K/V read rate, few queries against a long K/V (README.md:282-301)",
+        "value": round(rate_gbs / 1e3, 3), "unit": "TB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "settle": settle, "higher_is_better": True, "dtype": "fp16",
+        "data": "synthetic (seeded randn)",
+        "config": {"workload": f"pack-short: fp16 full B={c['B']} Hq={c['H_q']} Hkv={c['H_kv']} "
+                               f"N_q={n_q} N_kv={c['N_kv']} D={c['D']}",
+                   "n_q": n_q, "pack_gqa": should_pack_gqa(n_q, c["H_q"] // c["H_kv"], 128),
+                   "num_splits": splits},
+        "median_us": round(med * 1e3, 2),
+        "reference_h100_us": PACK_SHORT_H100_US.get(n_q),
+        "vs_reference_h100": (round(PACK_SHORT_H100_US[n_q] / (med * 1e3), 3)
+                              if n_q in PACK_SHORT_H100_US else None),
+        "roofline": {"bound": "hbm", "achieved": round(rate_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(rate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": kv},
+        "correctness_gate": {"max_abs_vs_sdpa": err, "sdpa_backend": backend},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description="MI355X FlashAttention-2 forward benchmark")
     ap.add_argument("--gpus", type=int, default=1)
@@ -314,6 +369,8 @@ def main():
     ap.add_argument("--config", default="C3", choices=sorted(WORKLOADS))
     ap.add_argument("--all", action="store_true", help="one line per GPU config C2..C5 (C3 first)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pack-short", action="store_true",
+                    help="instead of C3: the reference's few-queries table, one line per N_q")
     ap.add_argument("--flush-iters", type=int, default=10, help="iterations of the flushed pass (0: skip)")
     args = ap.parse_args()
 
@@ -328,6 +385,10 @@ def main():
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs the GPU")
+    if args.pack_short:
+        for n_q in sorted(PACK_SHORT_H100_US):
+            print(json.dumps(run_pack_short(n_q, args.steps, args.warmup)), flush=True)
+        return
     names = ["C3", "C2", "C4", "C5"] if args.all else [args.config]
     for i, name in enumerate(names):
         res = run(name, args.steps, args.warmup, with_cpu=(i == 0 and not args.no_cpu_baseline),

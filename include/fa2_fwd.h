@@ -15,6 +15,7 @@
 #ifndef FA2_FWD_H
 #define FA2_FWD_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -57,6 +58,49 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
                  int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
                  int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
                  int32_t block_m, int32_t block_n, float qk_scale, void* stream);
+
+/*
+ * fa2_attn_fwd_ex - fa2_attn_fwd with two optional extensions the reference does not have
+ * (its README.md:308-315 lists both as missing): the log-sum-exp of every row and split-KV.
+ * No counterpart in the reference's launch; fa2_attn_fwd(...) is fa2_attn_fwd_ex(...,
+ * NULL, 1, NULL, 0, stream).
+ *
+ *   lse        NULL, or device float[batch * h_q * n_q] (4-byte aligned), row
+ *              (b * h_q + h) * n_q + i: log sum_n exp(q_i . k_n * sm_scale) over the keys
+ *              row i sees, natural log (the softmax_lse of FlashAttention's backward).
+ *   num_splits 1..16. Above 1 (causal == 0 only), every program's key range is cut into
+ *              that many pieces of whole K/V tiles (fewer if the key range is shorter), one
+ *              workgroup each, and a second kernel merges the pieces. For grids too small
+ *              to fill the GPU: few queries against a long K/V. fa2_num_splits() picks it.
+ *   workspace  device memory of fa2_workspace_bytes(batch, h_q, n_q, head_dim, num_splits)
+ *              bytes, 256-byte aligned, when num_splits > 1 (else ignored; may be NULL). The
+ *              caller owns it; it must stay untouched until the launch has run.
+ */
+int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
+                    const int64_t q_stride[4], const int64_t k_stride[4],
+                    const int64_t v_stride[4], const int64_t o_stride[4],
+                    int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                    int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                    int32_t block_m, int32_t block_n, float qk_scale, float* lse,
+                    int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * fa2_workspace_bytes - workspace size of a split-KV launch of fa2_attn_fwd_ex: fp32 partial
+ * outputs and log-sum-exps of every split. 0 when num_splits <= 1 or a size is not positive.
+ */
+size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head_dim,
+                           int32_t num_splits);
+
+/*
+ * fa2_num_splits - the split count fa2_attn_fwd_ex should use: 1 for causal launches and for
+ * grids of at least num_cus workgroups; otherwise the smallest power of two that reaches it,
+ * keeping at least 4 K/V tiles per split, at most 16. The grid it sizes is the
+ * smaller of the packed and the unpacked GQA layouts, so the answer does not depend on the
+ * packing decision and packed and unpacked launches stay equal bit for bit. Host policy only.
+ */
+int32_t fa2_num_splits(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                       int32_t head_dim, int32_t causal, int32_t block_m, int32_t block_n,
+                       int32_t num_cus);
 
 /*
  * fa2_default_config - the gfx950 tile configuration for a head dim.

@@ -12,6 +12,10 @@ algorithm or helper it is named after:
                                                 the ground truth (callers pick fp32 or fp64)
   blocked_attention   fa2/reference.py:35-82    the kernel's tiled online-softmax recurrence
                                                 with fp32 state; the CPU baseline
+  naive_lse           (no counterpart)          log sum exp of the same masked, scaled scores
+                                                as naive_attention: the log-sum-exp output,
+                                                an extension the reference lacks (its
+                                                README.md:308), checked per row
   errors              tests/test_correctness.py:124-126   max-abs and relative-L2 error
   acceptance          tests/test_correctness.py:111-113, 172-185   ours <= 2 x SDPA + 1e-4
   attn_flops          bench/bench.py:83-87      4 B H_q pairs D, causal pairs N(N+1)/2
@@ -23,6 +27,11 @@ How each is pinned (tests/test_oracle.py; none of these restates the formula und
                       routine), closed forms (N=1 causal -> v[0]; one key -> v; equal scores ->
                       mean of v; a scale of 0 -> mean of v), GQA == MHA on repeated heads, and
                       planted mistakes (no mask, off-by-one mask, wrong KV head) that must fail.
+  naive_lse           an independent pure-Python float64 brute force (math.exp / math.log per
+                      row), closed forms (one key -> q.k * scale; a scale of 0 -> log of the
+                      visible-key count, i.e. log(i + 1) for causal row i; equal scores ->
+                      score + log N), and planted mistakes (mask dropped, base 2 instead of e)
+                      that must fail.
   blocked_attention   equal to naive_attention to 1e-5 in fp64 over the reference's own sweep
                       (tests/test_correctness.py:133-148), with planted mistakes (alpha dropped,
                       off-by-one causal mask) that must fail the same check.
@@ -73,6 +82,32 @@ def naive_attention(q, k, v, causal=True, sm_scale=None, heads_per_chunk=None):
         if causal:
             s = s.masked_fill(~mask, float("-inf"))
         out[:, h0:h1] = torch.matmul(torch.softmax(s, dim=-1), vc)
+        del s
+    return out
+
+
+def naive_lse(q, k, v, causal=True, sm_scale=None, heads_per_chunk=None):
+    """log sum_n exp(q_i . k_n * scale) over the keys row i sees, natural log, in q's dtype:
+    [B, H_q, N_q]. The scores and mask are naive_attention's (fa2/reference.py:22-32); the
+    reference has no log-sum-exp output. v is accepted for a uniform signature and unused."""
+    B, H_q, N_q, D = q.shape
+    H_kv, N_kv = k.shape[1], k.shape[2]
+    group = H_q // H_kv
+    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(D)
+    if heads_per_chunk is None:
+        per_head = B * N_q * N_kv * q.element_size()
+        heads_per_chunk = max(1, min(H_q, (2 << 30) // max(1, per_head)))
+    mask = None
+    if causal:
+        mask = torch.ones(N_q, N_kv, dtype=torch.bool, device=q.device).tril()
+    out = torch.empty(B, H_q, N_q, dtype=q.dtype, device=q.device)
+    for h0 in range(0, H_q, heads_per_chunk):
+        h1 = min(H_q, h0 + heads_per_chunk)
+        kc = k.index_select(1, torch.arange(h0, h1, device=q.device) // group)
+        s = torch.matmul(q[:, h0:h1], kc.transpose(-1, -2).contiguous()) * scale
+        if causal:
+            s = s.masked_fill(~mask, float("-inf"))
+        out[:, h0:h1] = torch.logsumexp(s, dim=-1)
         del s
     return out
 

@@ -178,3 +178,75 @@ def test_c_abi_rejects_bad_arguments(over, code, msg):
 def test_c_abi_empty_output_is_a_no_op():
     assert _call(batch=0, q=0, k=0, v=0, out=0)[0] == 0
     assert _call(n_q=0, n_kv=0, q=0, k=0, v=0, out=0)[0] == 0
+
+
+# ------------------------------------------------------------------------------------------
+# fa2_attn_fwd_ex: log-sum-exp output and split-KV (extensions; no reference counterpart)
+# ------------------------------------------------------------------------------------------
+
+def _call_ex(**over):
+    """fa2_attn_fwd_ex, non-causal, with fake pointers: every case below fails before a launch."""
+    a = dict(q=0x1000, k=0x2000, v=0x3000, out=0x4000, sq=(8192, 2048, 64, 1), sk=(65536, 16384, 64, 1),
+             sv=(65536, 16384, 64, 1), so=(8192, 2048, 64, 1), batch=1, h_q=4, h_kv=2, n_q=32, n_kv=256,
+             head_dim=64, dtype=0, causal=0, pack=1, block_m=128, block_n=64, qk_scale=0.18, lse=None,
+             num_splits=4, workspace=None, ws_bytes=0, stream=None)
+    a.update(over)
+    arr = lambda s: (ctypes.c_int64 * 4)(*s)  # noqa: E731
+    lib = _lib.lib()
+    rc = lib.fa2_attn_fwd_ex(a["q"], a["k"], a["v"], a["out"], arr(a["sq"]), arr(a["sk"]), arr(a["sv"]),
+                             arr(a["so"]), a["batch"], a["h_q"], a["h_kv"], a["n_q"], a["n_kv"],
+                             a["head_dim"], a["dtype"], a["causal"], a["pack"], a["block_m"],
+                             a["block_n"], a["qk_scale"], a["lse"], a["num_splits"], a["workspace"],
+                             a["ws_bytes"], a["stream"])
+    return rc, _lib.last_error()
+
+
+@needs_lib
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(num_splits=0), -1, "num_splits"),
+    (dict(num_splits=17), -1, "num_splits"),
+    (dict(causal=1, n_kv=32, sk=(8192, 2048, 64, 1), sv=(8192, 2048, 64, 1)), -1, "causal"),
+    (dict(workspace=None), -1, "workspace"),
+    (dict(workspace=0x100000, ws_bytes=1024), -1, "workspace"),
+    (dict(workspace=0x100010, ws_bytes=1 << 30), -2, "256-byte"),
+    (dict(lse=0x1002, num_splits=1), -2, "lse"),
+    (dict(head_dim=48), -1, "head_dim"),
+])
+def test_c_abi_ex_rejects_bad_arguments(over, code, msg):
+    rc, err = _call_ex(**over)
+    assert rc == code and msg in err, (rc, err)
+
+
+@needs_lib
+def test_split_policy():
+    lib = _lib.lib()
+    # the reference's pack-short regime (README.md:282-301), B=16, H 32/8, N_kv=4096, packed:
+    # N_q <= 32 -> 128 programs -> 4 splits fill 256 CUs twice; N_q = 64 -> 256 programs -> 2
+    # (the smaller grid is the packed one: 128 programs at N_q <= 32, 256 at N_q = 64)
+    for n_q, want in ((1, 2), (16, 2), (32, 2), (64, 1), (128, 1)):
+        assert lib.fa2_num_splits(16, 32, 8, n_q, 4096, 128, 0, 128, 64, 256) == want, n_q
+    assert lib.fa2_num_splits(16, 32, 8, 1, 4096, 128, 1, 128, 64, 256) == 1      # causal
+    assert lib.fa2_num_splits(16, 32, 8, 1, 4096, 128, 0, 127, 64, 256) == 1      # 127 % 4: 512 programs
+    assert lib.fa2_num_splits(1, 8, 8, 1, 256, 128, 0, 128, 64, 256) == 1         # 4 tiles only
+    assert lib.fa2_num_splits(1, 8, 8, 1, 512, 128, 0, 128, 64, 256) == 2         # 8 tiles: 2 x 4
+    assert lib.fa2_num_splits(1, 8, 8, 1, 4096, 128, 0, 128, 64, 256) == 16       # 8 programs, capped
+    assert lib.fa2_num_splits(4, 8, 8, 1, 4096, 128, 0, 128, 64, 256) == 8        # 32 x 8 = 256
+
+
+@needs_lib
+def test_workspace_bytes():
+    lib = _lib.lib()
+    rows = 16 * 32 * 1
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert lib.fa2_workspace_bytes(16, 32, 1, 128, 4) == up(4 * rows * 128 * 4) + up(4 * rows * 4)
+    assert lib.fa2_workspace_bytes(3, 5, 7, 16, 3) == up(3 * 105 * 16 * 4) + up(3 * 105 * 4)
+    assert lib.fa2_workspace_bytes(16, 32, 1, 128, 1) == 0
+    assert lib.fa2_workspace_bytes(16, 32, 0, 128, 4) == 0
+
+
+def test_split_and_lse_arguments_fail_in_python():
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="num_splits"):
+        attention(q, q, q, causal=False, num_splits=0)
+    with pytest.raises(ValueError, match="causal"):
+        attention(q, q, q, causal=True, num_splits=2)

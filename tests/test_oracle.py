@@ -234,3 +234,74 @@ def test_c1_blocked_meets_the_2x_bar_on_cpu():
     sdpa_abs, _ = ref.errors(sdpa, truth)
     assert torch.isfinite(ours).all()
     assert ref.acceptance(ours_abs, sdpa_abs), (ours_abs, sdpa_abs)
+
+
+# ------------------------------------------------------------------------------------------
+# naive_lse: the log-sum-exp output (an extension: the reference has none)
+# ------------------------------------------------------------------------------------------
+
+def _bruteforce_lse(q, k, causal, scale):
+    """Per-row log-sum-exp in pure-Python float64 (math.exp / math.log), GQA by index."""
+    B, H_q, N_q, D = q.shape
+    H_kv, N_kv = k.shape[1], k.shape[2]
+    group = H_q // H_kv
+    Q, K = q.tolist(), k.tolist()
+    out = torch.empty(B, H_q, N_q, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H_q):
+            for i in range(N_q):
+                scores = [sum(a * c for a, c in zip(Q[b][h][i], K[b][h // group][n])) * scale
+                          for n in range(N_kv) if not causal or n <= i]
+                m = max(scores)
+                out[b, h, i] = m + math.log(sum(math.exp(x - m) for x in scores))
+    return out
+
+
+LSE_CASES = [(True, 2, 1, 6, 6), (True, 4, 2, 9, 9), (False, 2, 2, 3, 11), (False, 4, 1, 7, 5)]
+
+
+def _lse_inputs(H_q, H_kv, N_q, N_kv, D=8, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(2, H_q, N_q, D, generator=g, dtype=torch.float64)
+    k = torch.randn(2, H_kv, N_kv, D, generator=g, dtype=torch.float64)
+    return q, k
+
+
+@pytest.mark.parametrize("causal,H_q,H_kv,N_q,N_kv", LSE_CASES)
+def test_lse_matches_bruteforce(causal, H_q, H_kv, N_q, N_kv):
+    q, k = _lse_inputs(H_q, H_kv, N_q, N_kv)
+    got = ref.naive_lse(q, k, k, causal=causal)
+    torch.testing.assert_close(got, _bruteforce_lse(q, k, causal, 1 / math.sqrt(8)), atol=1e-12, rtol=0)
+
+
+def test_lse_closed_forms():
+    q, k = _lse_inputs(4, 2, 6, 6)
+    # one key: the log-sum-exp is that key's scaled score
+    one = ref.naive_lse(q, k[:, :, :1], None, causal=False, sm_scale=0.3)
+    want = (q * k[:, [0, 0, 1, 1], :1]).sum(-1) * 0.3
+    torch.testing.assert_close(one, want, atol=1e-12, rtol=0)
+    # a scale of 0: every visible score is 0, so the result is log(#visible keys)
+    causal0 = ref.naive_lse(q, k, None, causal=True, sm_scale=0.0)
+    torch.testing.assert_close(causal0, torch.log(torch.arange(1, 7, dtype=torch.float64)).expand(2, 4, 6))
+    full0 = ref.naive_lse(q, k, None, causal=False, sm_scale=0.0)
+    torch.testing.assert_close(full0, torch.full((2, 4, 6), math.log(6), dtype=torch.float64))
+    # identical keys: every score equals s, so the result is s + log N
+    same = k[:, :, :1].expand(-1, -1, 6, -1).contiguous()
+    lse = ref.naive_lse(q, same, None, causal=False)
+    s = (q * same[:, [0, 0, 1, 1], :1]).sum(-1) / math.sqrt(8)
+    torch.testing.assert_close(lse, s + math.log(6), atol=1e-12, rtol=0)
+
+
+@pytest.mark.parametrize("kind", ["no_mask", "base_2"])
+def test_lse_check_catches_planted_mistakes(kind):
+    """The brute force fails a log-sum-exp with the causal mask dropped or taken in base 2."""
+    def planted(q, k, causal):
+        wrong = ref.naive_lse(q, k, None, causal=causal and kind != "no_mask")
+        return wrong / math.log(2) if kind == "base_2" else wrong
+    caught = False
+    for causal, H_q, H_kv, N_q, N_kv in LSE_CASES:
+        q, k = _lse_inputs(H_q, H_kv, N_q, N_kv)
+        if not torch.allclose(planted(q, k, causal), _bruteforce_lse(q, k, causal, 1 / math.sqrt(8)),
+                              atol=1e-9, rtol=0):
+            caught = True
+    assert caught, f"planted mistake {kind!r} slipped through"

@@ -13,6 +13,7 @@ namespace fa2 {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -26,6 +27,8 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 constexpr int kXcds = 8;
 // Lazy-rescale threshold in exp2 units: the reference max lags the true max by at most this.
 constexpr float kRescaleTau = 8.0f;
+// ln 2: a base-2 log-sum-exp times this is the natural one
+constexpr float kLn2 = 0.6931471805599453f;
 
 // ---------------------------------------------------------------------------------
 // element type traits: the MFMA and the fp32 -> 16-bit pair conversion (RNE)

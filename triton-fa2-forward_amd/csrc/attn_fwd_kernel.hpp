@@ -65,7 +65,9 @@ void attn_fwd_kernel(const Params p) {
   const int c = lane & 31;
   const int g = lane >> 5;
 
-  const Program pr = program_of<CAUSAL>(p, blockIdx.x);
+  // split-KV: consecutive workgroups are the splits of one program
+  const int split = p.splits > 1 ? (int)blockIdx.x % p.splits : 0;
+  const Program pr = program_of<CAUSAL>(p, p.splits > 1 ? (int)blockIdx.x / p.splits : (int)blockIdx.x);
 
   // ---- this lane's query row: packed row r -> (position r / pack, head r % pack)
   // (fa2/kernel.py:135-139). Rows past block_m or past n_q compute on zeros and are
@@ -91,15 +93,19 @@ void attn_fwd_kernel(const Params p) {
   // a whole tile); full: every whole tile. The rest is masked (stage 2 / the tail).
   const int pos_per_prog = p.block_m / p.pack;
   const int lo_pos = pr.tile * pos_per_prog;
-  int kv_end, full_end;
+  int kv_begin = 0, kv_end, full_end;
   if (CAUSAL) {
     kv_end = min(lo_pos + pos_per_prog, p.n_kv);
     full_end = (lo_pos / BN) * BN;
   } else {
     kv_end = p.n_kv;
     full_end = (p.n_kv / BN) * BN;
+    if (p.splits > 1) {  // this split's tiles (non-causal only; every split is non-empty)
+      kv_begin = split * p.split_tiles * BN;
+      kv_end = min(kv_begin + p.split_tiles * BN, p.n_kv);
+    }
   }
-  const int n_tiles_kv = (kv_end + BN - 1) / BN;
+  const int n_tiles_kv = (kv_end - kv_begin + BN - 1) / BN;
 
   // ---- K/V staging: each wave issues every NW-th 1 KiB load of the tile. Chunk P of a tile
   // (16 bytes, P = 64 * instruction + lane) holds row P / CPR, logical chunk
@@ -202,9 +208,9 @@ void attn_fwd_kernel(const Params p) {
   constexpr int NKP = LA_S * NB;               // K operand reads prefetched during PV
   u32x4 kop[LA_S][NB];
   if (n_tiles_kv > 0) {
-    issue_k(0, 0);
-    issue_v(0, 0);
-    if (n_tiles_kv > 1) issue_k(BN, 1);
+    issue_k(kv_begin, 0);
+    issue_v(kv_begin, 0);
+    if (n_tiles_kv > 1) issue_k(kv_begin + BN, 1);
     wait_vmcnt<0>();
     __syncthreads();
 #pragma unroll
@@ -213,7 +219,7 @@ void attn_fwd_kernel(const Params p) {
       for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand_v(0, ks, nb);
   }
   for (int j = 0; j < n_tiles_kv; ++j) {
-    const int n0 = j * BN;
+    const int n0 = kv_begin + j * BN;
     const int buf = j & 1;
 
     // S^T = K Q^T  (fa2/kernel.py:75-79). The two products run at raised wave priority and
@@ -324,20 +330,46 @@ void attn_fwd_kernel(const Params p) {
   // ---- normalise once, store once (fa2/kernel.py:178-183)
   const float l = pair_sum(l_i);
   if (row_ok) {
-    uint16_t* orow = p.o + pr.b * p.sob + head * p.soh + (int64_t)pos * p.son;
+    const int64_t row_index = ((int64_t)pr.b * p.h_q + head) * p.n_q + pos;  // in [B, H_q, N_q]
+    // log2 of this row's sum of exp2(s * qk_scale) over the keys seen: m is its reference
+    const float lse2 = m_i + log2f(l);
+    if (p.splits > 1) {
+      // split-KV: the normalised partial output (fp32) and its base-2 log-sum-exp
+      float* po = p.part_o + ((int64_t)split * p.part_rows + row_index) * D;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+      for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int d0 = 32 * db + 16 * h + 8 * g;
-        if (d0 < D) {
-          const u32x4 o = {E::pack2(acc[db][8 * h + 0] / l, acc[db][8 * h + 1] / l),
-                           E::pack2(acc[db][8 * h + 2] / l, acc[db][8 * h + 3] / l),
-                           E::pack2(acc[db][8 * h + 4] / l, acc[db][8 * h + 5] / l),
-                           E::pack2(acc[db][8 * h + 6] / l, acc[db][8 * h + 7] / l)};
-          *(u32x4*)(orow + d0) = o;
+        for (int h = 0; h < 2; ++h) {
+          const int d0 = 32 * db + 16 * h + 8 * g;
+          if (d0 < D) {
+            f32x4 lo, hi;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              lo[i] = acc[db][8 * h + i] / l;
+              hi[i] = acc[db][8 * h + 4 + i] / l;
+            }
+            *(f32x4*)(po + d0) = lo;
+            *(f32x4*)(po + d0 + 4) = hi;
+          }
         }
-      }
+      if (g == 0) p.part_lse[(int64_t)split * p.part_rows + row_index] = lse2;
+    } else {
+      uint16_t* orow = p.o + pr.b * p.sob + head * p.soh + (int64_t)pos * p.son;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int d0 = 32 * db + 16 * h + 8 * g;
+          if (d0 < D) {
+            const u32x4 o = {E::pack2(acc[db][8 * h + 0] / l, acc[db][8 * h + 1] / l),
+                             E::pack2(acc[db][8 * h + 2] / l, acc[db][8 * h + 3] / l),
+                             E::pack2(acc[db][8 * h + 4] / l, acc[db][8 * h + 5] / l),
+                             E::pack2(acc[db][8 * h + 6] / l, acc[db][8 * h + 7] / l)};
+            *(u32x4*)(orow + d0) = o;
+          }
+        }
+      if (p.lse && g == 0) p.lse[row_index] = lse2 * kLn2;
+    }
   }
 }
 

@@ -22,6 +22,9 @@ template <int DT, int D>
 int launch_attn_fwd_r64(const Params& p, int waves, int block_n, bool causal, unsigned grid,
                         hipStream_t stream);
 
+// Launches the split-KV combine pass (attn_fwd_combine.hip).
+int launch_combine(int dtype, int head_dim, const CombineParams& c, hipStream_t stream);
+
 #define FA2_DECLARE_LAUNCH(DT, D)                                                          \
   extern template int launch_attn_fwd<DT, D>(const Params&, int, int, bool, unsigned, \
                                              hipStream_t);

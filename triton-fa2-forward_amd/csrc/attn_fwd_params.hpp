@@ -23,6 +23,27 @@ struct Params {
   int32_t n_tiles;  // programs along the packed rows: ceil(n_q * pack / block_m)
   int32_t n_bh;     // programs along batch x head groups: batch * h_q / pack
   float qk_scale;   // sm_scale * log2(e)
+  // Optional outputs beyond the reference's:
+  float* lse;        // [B, H_q, N_q] natural-log log-sum-exp of the scaled scores, or null
+  // Split-KV: the key range of every program is cut into `splits` pieces of `split_tiles`
+  // K/V tiles, one workgroup each; each writes its normalised partial output and base-2
+  // log-sum-exp, which a combine pass merges (splits == 1: the kernel writes o itself).
+  float* part_o;     // [splits][B * H_q * N_q][D] fp32
+  float* part_lse;   // [splits][B * H_q * N_q] fp32, base 2
+  int64_t part_rows; // B * H_q * N_q
+  int32_t splits;
+  int32_t split_tiles;
+};
+
+// Arguments of the split-KV combine pass: rows are the [B, H_q, N_q] rows of the output.
+struct CombineParams {
+  const float* part_o;    // [splits][rows][D]
+  const float* part_lse;  // [splits][rows], base 2
+  uint16_t* o;
+  float* lse;             // optional natural-log log-sum-exp [rows]
+  int64_t sob, soh, son;
+  int64_t rows;
+  int32_t h_q, n_q, splits;
 };
 
 }  // namespace fa2

@@ -2,7 +2,8 @@
 
     python triton-fa2-forward_amd/csrc/build.py [-j 8] [--verbose]
 
-Compiles attn_fwd_inst.hip once per (dtype, head_dim) pair plus the C-ABI file fa2_fwd.hip,
+Compiles attn_fwd_inst.hip once per (dtype, head_dim) pair plus the split-KV combine pass
+(attn_fwd_combine.hip) and the C-ABI file fa2_fwd.hip,
 in parallel, with hipcc for gfx950 only, and links them into
 triton-fa2-forward_amd/fa2/libfa2_fwd.so next to the Python front end that loads it.
 """
@@ -64,8 +65,9 @@ def build(jobs=8, verbose=False):
             obj = os.path.join(OBJ_DIR, f"attn_fwd_dt{dt}_d{d}.o")
             units.append([cc, *common_flags(), f"-DFA2_DT={dt}", f"-DFA2_D={d}", "-c",
                           os.path.join(CSRC, "attn_fwd_inst.hip"), "-o", obj])
-    api_obj = os.path.join(OBJ_DIR, "fa2_fwd.o")
-    units.append([cc, *common_flags(), "-c", os.path.join(CSRC, "fa2_fwd.hip"), "-o", api_obj])
+    for name in ("attn_fwd_combine", "fa2_fwd"):
+        units.append([cc, *common_flags(), "-c", os.path.join(CSRC, name + ".hip"),
+                      "-o", os.path.join(OBJ_DIR, name + ".o")])
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(lambda cmd: _run(cmd, verbose), units))
     objs = [u[-1] for u in units]

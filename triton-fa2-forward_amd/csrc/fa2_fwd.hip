@@ -7,6 +7,7 @@
 // launch it out of bounds.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -65,6 +66,30 @@ int dim_index(int d) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// block_n request -> the K/V tile width the kernels are built for (0 = default 64)
+int tile_n(int block_n) {
+  const int req = block_n ? block_n : 64;
+  return req <= 32 ? 32 : req <= 64 ? 64 : 128;
+}
+
+// Split-KV limits: at most 16 splits, and a split of fewer than 4 K/V tiles is not worth a
+// workgroup (its fixed cost, Q load and output write, would dominate).
+constexpr int kMaxSplits = 16;
+constexpr int kMinSplitTiles = 4;
+
+// Workspace of a split-KV launch: partial outputs, then partial log-sum-exps, 256-byte aligned.
+struct WorkspaceLayout {
+  size_t part_o, part_lse, total;
+};
+WorkspaceLayout workspace_layout(size_t rows, int head_dim, int splits) {
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  WorkspaceLayout w;
+  w.part_o = 0;
+  w.part_lse = up((size_t)splits * rows * head_dim * sizeof(float));
+  w.total = w.part_lse + up((size_t)splits * rows * sizeof(float));
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
@@ -102,6 +127,47 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
                  int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
                  int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
                  int32_t block_m, int32_t block_n, float qk_scale, void* stream) {
+  return fa2_attn_fwd_ex(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                         n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale,
+                         nullptr, 1, nullptr, 0, stream);
+}
+
+size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head_dim,
+                           int32_t num_splits) {
+  if (num_splits <= 1 || batch <= 0 || h_q <= 0 || n_q <= 0 || dim_index(head_dim) < 0) return 0;
+  const size_t rows = (size_t)batch * h_q * n_q;
+  return workspace_layout(rows, head_dim, num_splits).total;
+}
+
+int32_t fa2_num_splits(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                       int32_t head_dim, int32_t causal, int32_t block_m, int32_t block_n,
+                       int32_t num_cus) {
+  if (causal || batch <= 0 || h_q <= 0 || h_kv <= 0 || h_q % h_kv || n_q <= 0 || n_kv <= 0 ||
+      block_m <= 0 || num_cus <= 0 || dim_index(head_dim) < 0)
+    return 1;
+  // The grid of the smaller of the two GQA layouts, so that a packed and an unpacked launch
+  // of the same problem split the same way and stay equal bit for bit.
+  const int group = h_q / h_kv;
+  int64_t programs = ((int64_t)n_q + block_m - 1) / block_m * ((int64_t)batch * h_q);
+  if (block_m % group == 0)
+    programs = std::min(programs, ((int64_t)n_q * group + block_m - 1) / block_m * ((int64_t)batch * h_kv));
+  const int bn = tile_n(block_n);
+  const int64_t tiles = ((int64_t)n_kv + bn - 1) / bn;
+  // Split until every CU has a workgroup, with at least kMinSplitTiles tiles per split and at
+  // most kMaxSplits splits. (Filling the second workgroup slot of each CU as well measured
+  // slower on MI355X: the fp32 partial outputs cost more than the extra overlap gains.)
+  int s = 1;
+  while (programs * s < num_cus && s * 2 <= kMaxSplits && tiles / (s * 2) >= kMinSplitTiles) s *= 2;
+  return s;
+}
+
+int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
+                    const int64_t q_stride[4], const int64_t k_stride[4],
+                    const int64_t v_stride[4], const int64_t o_stride[4],
+                    int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                    int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                    int32_t block_m, int32_t block_n, float qk_scale, float* lse,
+                    int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = '\0';
   // ---- shape checks (fa2/kernel.py:218-228)
   if (batch < 0 || h_q <= 0 || h_kv <= 0 || n_q < 0 || n_kv < 0)
@@ -130,6 +196,11 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
   if (!(qk_scale > 0.f) || !std::isfinite(qk_scale))
     return fail(FA2_EINVAL, "qk_scale (sm_scale * log2 e) must be positive and finite, got %g",
                 (double)qk_scale);
+  // ---- split-KV
+  if (num_splits < 1 || num_splits > kMaxSplits)
+    return fail(FA2_EINVAL, "num_splits must be in [1, %d], got %d", kMaxSplits, num_splits);
+  if (num_splits > 1 && causal)
+    return fail(FA2_EINVAL, "split-KV needs causal == 0 (the causal kernel skips tiles instead)");
   if (batch == 0 || n_q == 0) return FA2_OK;  // empty output: nothing to launch
   // ---- the 16-byte load/store rule
   if (!q || !k || !v || !out) return fail(FA2_EINVAL, "null tensor pointer");
@@ -146,6 +217,8 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
         return fail(FA2_EALIGN, "strides must be multiples of 8 elements (tensor %d dim %d: %lld)",
                     t, j, (long long)strides[t][j]);
   }
+  if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u))
+    return fail(FA2_EALIGN, "lse must be 4-byte aligned");
   // K/V tiles are addressed with 32-bit byte offsets from the tile's first row.
   if (k_stride[2] > kMaxRowStride || v_stride[2] > kMaxRowStride)
     return fail(FA2_EINVAL, "k/v sequence stride above %lld elements is not supported",
@@ -155,8 +228,7 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
   // computed on zeros and dropped); block_n -> the next supported K/V tile width.
   int waves = 1;
   while (waves * 32 < block_m) waves *= 2;
-  const int bn_req = block_n ? block_n : 64;
-  const int bn = bn_req <= 32 ? 32 : bn_req <= 64 ? 64 : 128;
+  const int bn = tile_n(block_n);
 
   Params p;
   p.q = static_cast<const uint16_t*>(q);
@@ -176,21 +248,65 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
   const int64_t rows = (int64_t)n_q * pack;
   const int64_t n_tiles = (rows + block_m - 1) / block_m;
   const int64_t n_bh = (int64_t)batch * (h_q / pack);
-  if (n_tiles * n_bh > 0x7fffffffLL)
-    return fail(FA2_EINVAL, "grid of %lld programs is too large", (long long)(n_tiles * n_bh));
   p.n_tiles = (int32_t)n_tiles;
   p.n_bh = (int32_t)n_bh;
   p.qk_scale = qk_scale;
+  p.lse = lse;
+  p.part_o = nullptr;
+  p.part_lse = nullptr;
+  p.part_rows = (int64_t)batch * h_q * n_q;
+  p.splits = 1;
+  p.split_tiles = 0;
+
+  // Split-KV: cut the key range into whole tiles; drop splits that would be empty.
+  const int64_t kv_tiles = ((int64_t)n_kv + bn - 1) / bn;
+  int splits = num_splits;
+  if (splits > 1 && kv_tiles > 0) {
+    const int64_t per = (kv_tiles + splits - 1) / splits;
+    splits = (int)((kv_tiles + per - 1) / per);
+    p.split_tiles = (int32_t)per;
+  }
+  if (splits <= 1 || n_kv == 0) splits = 1;
+  if (splits > 1) {
+    const WorkspaceLayout w = workspace_layout((size_t)p.part_rows, head_dim, splits);
+    if (!workspace || workspace_bytes < w.total)
+      return fail(FA2_EINVAL, "split-KV with %d splits needs a workspace of %zu bytes, got %zu",
+                  splits, w.total, workspace ? workspace_bytes : (size_t)0);
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+      return fail(FA2_EALIGN, "the workspace must be 256-byte aligned");
+    p.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.part_o);
+    p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.part_lse);
+    p.splits = splits;
+  }
+  const int64_t grid = n_tiles * n_bh * splits;
+  if (grid > 0x7fffffffLL)
+    return fail(FA2_EINVAL, "grid of %lld workgroups is too large", (long long)grid);
 
   // Programs of 128 or 256 rows over 32-key tiles at head_dim 64/128 run the kernel with 64
-  // query rows per wave (half the LDS traffic per FLOP); everything else the 32-row kernel.
-  const bool r64 = head_dim >= 64 && (block_m == 128 || block_m == 256) && bn == 32;
-  const int e = r64 ? launch_r64(dtype, di, p, block_m / 64, causal != 0,
-                                 (unsigned)(n_tiles * n_bh), static_cast<hipStream_t>(stream))
-                    : launch(dtype, di, p, waves, bn, causal != 0, (unsigned)(n_tiles * n_bh),
-                             static_cast<hipStream_t>(stream));
+  // query rows per wave; everything else, and every launch that writes the log-sum-exp or
+  // splits the key range, the 32-row kernel.
+  const bool r64 = head_dim >= 64 && (block_m == 128 || block_m == 256) && bn == 32 && !lse &&
+                   splits == 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int e = r64 ? launch_r64(dtype, di, p, block_m / 64, causal != 0, (unsigned)grid, st)
+              : launch(dtype, di, p, waves, bn, causal != 0, (unsigned)grid, st);
   if (e != hipSuccess)
     return fail(FA2_ELAUNCH, "kernel launch failed: %s", hipGetErrorString((hipError_t)e));
+  if (splits > 1) {
+    fa2::CombineParams c;
+    c.part_o = p.part_o;
+    c.part_lse = p.part_lse;
+    c.o = p.o;
+    c.lse = lse;
+    c.sob = p.sob; c.soh = p.soh; c.son = p.son;
+    c.rows = p.part_rows;
+    c.h_q = h_q;
+    c.n_q = n_q;
+    c.splits = splits;
+    e = fa2::launch_combine(dtype, head_dim, c, st);
+    if (e != hipSuccess)
+      return fail(FA2_ELAUNCH, "combine launch failed: %s", hipGetErrorString((hipError_t)e));
+  }
   return FA2_OK;
 }
 

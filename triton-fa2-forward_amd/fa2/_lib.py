@@ -19,6 +19,12 @@ SIGNATURES = {
     "fa2_attn_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
                                     _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                     _i32, _i32, ctypes.c_float, _vp]),
+    "fa2_attn_fwd_ex": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
+                                       _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                       _i32, _i32, ctypes.c_float, _vp, _i32, _vp,
+                                       ctypes.c_size_t, _vp]),
+    "fa2_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
+    "fa2_num_splits": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "fa2_default_config": (ctypes.c_int, [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                           ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "fa2_should_pack_gqa": (ctypes.c_int, [_i32, _i32, _i32]),
@@ -69,3 +75,28 @@ def attn_fwd(q, k, v, out, causal, pack, block_m, block_n, qk_scale, stream):
         block_m, block_n, qk_scale, stream)
     if rc != 0:
         raise RuntimeError(f"fa2_attn_fwd failed ({rc}): {last_error()}")
+
+
+def attn_fwd_ex(q, k, v, out, causal, pack, block_m, block_n, qk_scale, lse, num_splits,
+                workspace, stream):
+    """Call fa2_attn_fwd_ex: lse (fp32 [B, H_q, N_q]) and workspace (uint8) may be None."""
+    B, H_q, N_q, D = q.shape
+    H_kv, N_kv = k.shape[1], k.shape[2]
+    rc = lib().fa2_attn_fwd_ex(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+        _strides(q), _strides(k), _strides(v), _strides(out),
+        B, H_q, H_kv, N_q, N_kv, D, DTYPE_CODE[q.dtype], int(bool(causal)), pack,
+        block_m, block_n, qk_scale, None if lse is None else lse.data_ptr(), num_splits,
+        None if workspace is None else workspace.data_ptr(),
+        0 if workspace is None else workspace.numel(), stream)
+    if rc != 0:
+        raise RuntimeError(f"fa2_attn_fwd_ex failed ({rc}): {last_error()}")
+
+
+def workspace_bytes(B, H_q, N_q, D, num_splits):
+    return int(lib().fa2_workspace_bytes(B, H_q, N_q, D, num_splits))
+
+
+def num_splits(B, H_q, H_kv, N_q, N_kv, D, causal, block_m, block_n, num_cus):
+    return int(lib().fa2_num_splits(B, H_q, H_kv, N_q, N_kv, D, int(bool(causal)), block_m,
+                                    block_n, num_cus))

@@ -64,13 +64,31 @@ def _loadable(t):
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
+_CU_COUNT = {}
+
+
+def _cu_count(device):
+    if device not in _CU_COUNT:
+        _CU_COUNT[device] = torch.cuda.get_device_properties(device).multi_processor_count
+    return _CU_COUNT[device]
+
+
 def attention(q, k, v, causal=True, sm_scale=None, block_m=None, block_n=None,
-              num_warps=None, num_stages=None, pack_gqa=None):
+              num_warps=None, num_stages=None, pack_gqa=None, *, num_splits=None,
+              return_lse=False):
     """softmax(Q K^T * sm_scale [+ causal mask]) V, fused (fa2/kernel.py:210-260).
 
     q: [B, H_q, N_q, D]; k, v: [B, H_kv, N_kv, D]; returns [B, H_q, N_q, D] laid out like q.
     pack_gqa: put each GQA group's query heads into one program; None decides with
     should_pack_gqa.
+
+    Keyword-only extensions (the reference has neither, README.md:308-315):
+    num_splits: split-KV, cut every program's key range into this many workgroups and merge
+        their partial results in a second kernel (non-causal only); None picks it from the
+        grid size and the GPU's CU count (1 when the grid already fills the GPU). The pick
+        does not depend on pack_gqa, so packed and unpacked results stay equal bit for bit.
+    return_lse: also return the natural-log log-sum-exp of every row's scaled scores, fp32
+        [B, H_q, N_q], i.e. (out, lse).
     """
     assert q.dim() == k.dim() == v.dim() == 4
     B, H_q, N_q, D = q.shape
@@ -98,20 +116,36 @@ def attention(q, k, v, causal=True, sm_scale=None, block_m=None, block_n=None,
     if not sm_scale > 0:
         raise ValueError(f"sm_scale must be positive (the row max is scaled after it is taken), got {sm_scale}")
     qk_scale = sm_scale * LOG2E  # exp(x) == exp2(x * log2 e)
+    if num_splits is not None:
+        if not 1 <= num_splits <= 16:
+            raise ValueError(f"num_splits must be in [1, 16], got {num_splits}")
+        if num_splits > 1 and causal:
+            raise ValueError("num_splits > 1 (split-KV) needs causal=False")
 
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise RuntimeError("fa2.kernel.attention runs on the GPU (gfx950 HIP kernel); got CPU tensors")
     if not (q.device == k.device == v.device):
         raise RuntimeError(f"q, k, v must be on one device, got {q.device}, {k.device}, {v.device}")
 
+    if num_splits is None:
+        num_splits = 1 if causal else _lib.num_splits(B, H_q, H_kv, N_q, N_kv, D, causal, bm, bn,
+                                                      _cu_count(q.device))
+
     out = torch.empty_like(q)
+    lse = torch.empty((B, H_q, N_q), dtype=torch.float32, device=q.device) if return_lse else None
     if out.numel() == 0:
-        return out
+        return (out, lse) if return_lse else out
     q_, k_, v_ = _loadable(q), _loadable(k), _loadable(v)
     o_ = _loadable(out)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        _lib.attn_fwd(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, stream)
+        if num_splits == 1 and lse is None:
+            _lib.attn_fwd(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, stream)
+        else:
+            ws_bytes = _lib.workspace_bytes(B, H_q, N_q, D, num_splits)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+            _lib.attn_fwd_ex(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, lse, num_splits,
+                             ws, stream)
     if o_ is not out:
         out.copy_(o_)
-    return out
+    return (out, lse) if return_lse else out
