@@ -3,6 +3,10 @@ bench/profile_target.py).
 
     python triton-fa2-forward_amd/profile_target.py --config C3 --launches 3
     python triton-fa2-forward_amd/profile_target.py --config C3 --launches 3 --copy-mib 1024
+    python triton-fa2-forward_amd/profile_target.py --pack-short 1 --launches 20
+
+--pack-short N_Q runs the reference's few-queries shape instead (bench.py --pack-short: fp16,
+B 16, H 32/8, N_kv 4096, D 128, non-causal, default path: packed, automatic split-KV).
 
 --copy-mib adds one plain device-to-device copy of that many MiB after the attention launches.
 Its FETCH_SIZE / WRITE_SIZE reading, against the bytes it is known to move, is the scale factor
@@ -25,6 +29,7 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0)
     ap.add_argument("--block-m", type=int, default=None)
     ap.add_argument("--block-n", type=int, default=None)
+    ap.add_argument("--pack-short", type=int, default=None, metavar="N_Q")
     args = ap.parse_args()
 
     import torch
@@ -32,8 +37,17 @@ def main():
     import bench
     from fa2.kernel import attention
 
-    q, k, v, causal = bench.make_inputs(args.config, "cuda")
-    print(f"profile_target: {bench.describe(args.config)}, {args.launches} launches", flush=True)
+    if args.pack_short is not None:
+        c = bench.PACK_SHORT
+        g = torch.Generator(device="cpu").manual_seed(0)
+        q = torch.randn(c["B"], c["H_q"], args.pack_short, c["D"], generator=g).half().cuda()
+        k = torch.randn(c["B"], c["H_kv"], c["N_kv"], c["D"], generator=g).half().cuda()
+        v = torch.randn(c["B"], c["H_kv"], c["N_kv"], c["D"], generator=g).half().cuda()
+        causal = False
+        print(f"profile_target: pack-short N_q={args.pack_short}, {args.launches} launches", flush=True)
+    else:
+        q, k, v, causal = bench.make_inputs(args.config, "cuda")
+        print(f"profile_target: {bench.describe(args.config)}, {args.launches} launches", flush=True)
     for _ in range(args.launches):
         attention(q, k, v, causal=causal, block_m=args.block_m, block_n=args.block_n)
     torch.cuda.synchronize()
