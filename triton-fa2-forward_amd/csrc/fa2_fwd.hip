@@ -66,9 +66,13 @@ int dim_index(int d) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// block_n request -> the K/V tile width the kernels are built for (0 = default 64)
-int tile_n(int block_n) {
-  const int req = block_n ? block_n : 64;
+// gfx950 default K/V tile (sweep.py on the BASELINE.json configs, MI355X): 64 keys at
+// head_dim 128 (C2, C3, C5 best), 128 keys at head_dim 64 (C4: 900 vs 857 TFLOP/s).
+int default_block_n(int head_dim) { return head_dim == 64 ? 128 : 64; }
+
+// block_n request -> the K/V tile width the kernels are built for (0 = the default)
+int tile_n(int block_n, int head_dim) {
+  const int req = block_n ? block_n : default_block_n(head_dim);
   return req <= 32 ? 32 : req <= 64 ? 64 : 128;
 }
 
@@ -102,10 +106,10 @@ int fa2_default_config(int32_t head_dim, int32_t* block_m, int32_t* block_n,
                        int32_t* num_waves, int32_t* num_stages) {
   if (dim_index(head_dim) < 0)
     return fail(FA2_EINVAL, "head_dim must be one of 16, 32, 64, 128, got %d", head_dim);
-  // gfx950 defaults: 4 wave64s of 32 query rows, 64-key K/V tiles, one tile in LDS
-  // while the next is in flight in registers.
+  // gfx950 defaults: 4 wave64s of 32 query rows, default_block_n keys per K/V tile, two K
+  // and two V tiles in LDS.
   if (block_m) *block_m = 128;
-  if (block_n) *block_n = 64;
+  if (block_n) *block_n = default_block_n(head_dim);
   if (num_waves) *num_waves = 4;
   if (num_stages) *num_stages = 2;
   return FA2_OK;
@@ -151,7 +155,7 @@ int32_t fa2_num_splits(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, in
   int64_t programs = ((int64_t)n_q + block_m - 1) / block_m * ((int64_t)batch * h_q);
   if (block_m % group == 0)
     programs = std::min(programs, ((int64_t)n_q * group + block_m - 1) / block_m * ((int64_t)batch * h_kv));
-  const int bn = tile_n(block_n);
+  const int bn = tile_n(block_n, head_dim);
   const int64_t tiles = ((int64_t)n_kv + bn - 1) / bn;
   // Split until every CU has a workgroup, with at least kMinSplitTiles tiles per split and at
   // most kMaxSplits splits. (Filling the second workgroup slot of each CU as well measured
@@ -228,7 +232,7 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
   // computed on zeros and dropped); block_n -> the next supported K/V tile width.
   int waves = 1;
   while (waves * 32 < block_m) waves *= 2;
-  const int bn = tile_n(block_n);
+  const int bn = tile_n(block_n, head_dim);
 
   Params p;
   p.q = static_cast<const uint16_t*>(q);

@@ -53,6 +53,9 @@ def main():
             except Exception as e:  # noqa: BLE001 - report and skip the variant
                 print(f"skip block_m={bm} block_n={bn}: {e}", flush=True)
     stream = torch.cuda.current_stream()
+    # settle the clocks first (bench.py's settle phase): otherwise the first rounds run in the
+    # ramp after the idle correctness checks
+    bench.settle_clocks(lambda: attention(q, k, v, causal=causal))
     samples = {vv: [] for vv in variants}
     for r in range(args.rounds):
         for bm, bn in variants:
