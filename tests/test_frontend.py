@@ -238,8 +238,9 @@ def test_workspace_bytes():
     lib = _lib.lib()
     rows = 16 * 32 * 1
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert lib.fa2_workspace_bytes(16, 32, 1, 128, 4) == up(4 * rows * 128 * 4) + up(4 * rows * 4)
-    assert lib.fa2_workspace_bytes(3, 5, 7, 16, 3) == up(3 * 105 * 16 * 4) + up(3 * 105 * 4)
+    # fp32 partial outputs, then two fp32 partial log-sum-exps (merge weights, exact), each aligned
+    assert lib.fa2_workspace_bytes(16, 32, 1, 128, 4) == up(4 * rows * 128 * 4) + 2 * up(4 * rows * 4)
+    assert lib.fa2_workspace_bytes(3, 5, 7, 16, 3) == up(3 * 105 * 16 * 4) + 2 * up(3 * 105 * 4)
     assert lib.fa2_workspace_bytes(16, 32, 1, 128, 1) == 0
     assert lib.fa2_workspace_bytes(16, 32, 0, 128, 4) == 0
 

@@ -1,10 +1,13 @@
 // attn_fwd_combine.hip - merges the partial outputs of a split-KV launch.
 //
 // Split s of a row saw keys K_s and wrote O_s = sum_{n in K_s} p_n v_n / l_s (fp32) and
-// lse_s = log2 sum_{n in K_s} exp2(s_n * qk_scale). With L = max_s lse_s and w_s = exp2(lse_s - L),
-//   O = sum_s w_s O_s / sum_s w_s,   lse = L + log2 sum_s w_s,
+// lse_s = log2 l_s, with p_n = exp2(s_n * qk_scale) rounded to the input type and l_s their sum
+// (the weights the kernel normalises by). With L = max_s lse_s and w_s = exp2(lse_s - L),
+//   O = sum_s w_s O_s / sum_s w_s,
 // the same online-softmax merge the kernel applies tile by tile (fa2/kernel.py:95-105), applied
-// once across splits. Memory-bound: each thread merges 4 dims of one row (16-byte loads).
+// once across splits; it equals the single-pass result up to rounding. The log-sum-exp output
+// merges the splits' exact (unrounded) lse the same way: L' + log2 sum_s exp2(lse'_s - L').
+// Memory-bound: each thread merges 4 dims of one row (16-byte loads).
 #include <hip/hip_runtime.h>
 
 #include "attn_fwd_common.hpp"
@@ -39,7 +42,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams c
   const int head = (int)(bh - b * c.h_q);
   uint16_t* orow = c.o + b * c.sob + head * c.soh + pos * c.son + d0;
   *(u32x2*)orow = u32x2{E::pack2(o[0] / wsum, o[1] / wsum), E::pack2(o[2] / wsum, o[3] / wsum)};
-  if (c.lse && d0 == 0) c.lse[row] = (L + log2f(wsum)) * kLn2;
+  if (c.lse && d0 == 0) {
+    float Lx = -INFINITY;
+    for (int s = 0; s < c.splits; ++s) Lx = fmaxf(Lx, c.part_lse_exact[s * c.rows + row]);
+    float sx = 0.f;
+    for (int s = 0; s < c.splits; ++s) sx += exp2f(c.part_lse_exact[s * c.rows + row] - Lx);
+    c.lse[row] = (Lx + log2f(sx)) * kLn2;
+  }
 }
 
 template <int DT, int D>

@@ -31,7 +31,8 @@ constexpr float kRescaleTau = 8.0f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 // ---------------------------------------------------------------------------------
-// element type traits: the MFMA and the fp32 -> 16-bit pair conversion (RNE)
+// element type traits: the MFMA, the fp32 -> 16-bit pair conversion (RNE) and the fp32 sum of
+// a converted pair
 // ---------------------------------------------------------------------------------
 template <int DT>
 struct Elem;
@@ -46,6 +47,11 @@ struct Elem<0> {  // fp16
     f16x2 v = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, v);
   }
+  // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_f16 against (1, 1))
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair),
+                                  __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
+  }
 };
 
 template <>
@@ -57,6 +63,11 @@ struct Elem<1> {  // bf16
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     bf16x2 v = {(__bf16)lo, (__bf16)hi};
     return __builtin_bit_cast(uint32_t, v);
+  }
+  // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_bf16 against (1, 1))
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
+                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
   }
 };
 

@@ -187,9 +187,18 @@ void attn_fwd_kernel(const Params p) {
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
 
-  // ---- online-softmax state (fa2/kernel.py:146-148); l is a per-lane partial sum
+  // ---- online-softmax state (fa2/kernel.py:146-148); l is a per-lane partial sum.
+  // bf16: l sums P rounded to bf16, the weights the PV product uses, so that O = acc / l is a
+  // convex combination of V rows. With the lazy reference max a row's largest P is 2^x, not 1,
+  // and its bf16 rounding (2^-9) would otherwise reach a row dominated by one key in full
+  // (C5's outlier keys: 1.74x SDPA's error with the fp32 sum, 0.93x with this one). l_exact then
+  // sums the unrounded P for the log-sum-exp output. fp16 rounds P 8x finer: l sums the fp32 P
+  // there, as the reference does (fa2/kernel.py:98), and is itself the exact sum.
+  constexpr bool kRoundedSum = DT == 1;
   float m_i = -INFINITY;
   float l_i = 0.f;
+  float l_exact = 0.f;
+  const bool want_exact = kRoundedSum && p.lse != nullptr;
   f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
@@ -280,20 +289,31 @@ void attn_fwd_kernel(const Params p) {
       const float m_new = grow ? mx : m_i;
       const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
       l_i *= alpha;
+      l_exact *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db) acc[db] *= alpha;
       m_i = m_new;
     }
-    float rs = 0.f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][i], qk_scale, -m_i));
-        s[nb][i] = e;
-        rs += e;
-      }
-    l_i += rs;
+      for (int i = 0; i < 16; ++i)
+        s[nb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][i], qk_scale, -m_i));
+    if constexpr (!kRoundedSum) {
+      float rs = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) rs += s[nb][i];
+      l_i += rs;
+    } else if (want_exact) {
+      float rx = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) rx += s[nb][i];
+      l_exact += rx;
+    }
 
     // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
     u32x4 pb[BN / 16];
@@ -304,6 +324,17 @@ void attn_fwd_kernel(const Params p) {
                     E::pack2(s[nb][8 * h + 2], s[nb][8 * h + 3]),
                     E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
                     E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
+    }
+    if constexpr (kRoundedSum) {
+      float rs0 = 0.f, rs1 = 0.f;
+#pragma unroll
+      for (int t = 0; t < BN / 16; ++t) {
+        rs0 = E::sum2(pb[t][0], rs0);
+        rs1 = E::sum2(pb[t][1], rs1);
+        rs0 = E::sum2(pb[t][2], rs0);
+        rs1 = E::sum2(pb[t][3], rs1);
+      }
+      l_i += rs0 + rs1;
     }
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -329,10 +360,14 @@ void attn_fwd_kernel(const Params p) {
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
   const float l = pair_sum(l_i);
+  const float lx = want_exact ? pair_sum(l_exact) : l;
   if (row_ok) {
     const int64_t row_index = ((int64_t)pr.b * p.h_q + head) * p.n_q + pos;  // in [B, H_q, N_q]
-    // log2 of this row's sum of exp2(s * qk_scale) over the keys seen: m is its reference
+    // log2 of this row's sum of the weights O is normalised by (exp2(s * qk_scale) rounded to
+    // the input type) and of the exact exp2(s * qk_scale), over the keys seen; m is their
+    // reference
     const float lse2 = m_i + log2f(l);
+    const float lse2_exact = m_i + log2f(lx);
     if (p.splits > 1) {
       // split-KV: the normalised partial output (fp32) and its base-2 log-sum-exp
       float* po = p.part_o + ((int64_t)split * p.part_rows + row_index) * D;
@@ -352,7 +387,10 @@ void attn_fwd_kernel(const Params p) {
             *(f32x4*)(po + d0 + 4) = hi;
           }
         }
-      if (g == 0) p.part_lse[(int64_t)split * p.part_rows + row_index] = lse2;
+      if (g == 0) {
+        p.part_lse[(int64_t)split * p.part_rows + row_index] = lse2;
+        if (p.lse) p.part_lse_exact[(int64_t)split * p.part_rows + row_index] = lse2_exact;
+      }
     } else {
       uint16_t* orow = p.o + pr.b * p.sob + head * p.soh + (int64_t)pos * p.son;
 #pragma unroll
@@ -368,7 +406,7 @@ void attn_fwd_kernel(const Params p) {
             *(u32x4*)(orow + d0) = o;
           }
         }
-      if (p.lse && g == 0) p.lse[row_index] = lse2 * kLn2;
+      if (p.lse && g == 0) p.lse[row_index] = lse2_exact * kLn2;
     }
   }
 }

@@ -24,12 +24,15 @@ struct Params {
   int32_t n_bh;     // programs along batch x head groups: batch * h_q / pack
   float qk_scale;   // sm_scale * log2(e)
   // Optional outputs beyond the reference's:
-  float* lse;        // [B, H_q, N_q] natural-log log-sum-exp of the scaled scores, or null
+  float* lse;        // [B, H_q, N_q] natural-log log-sum-exp of the scaled scores, or null;
+                     // when set, the kernel also sums the unrounded P (part_lse_exact)
   // Split-KV: the key range of every program is cut into `splits` pieces of `split_tiles`
   // K/V tiles, one workgroup each; each writes its normalised partial output and base-2
   // log-sum-exp, which a combine pass merges (splits == 1: the kernel writes o itself).
   float* part_o;     // [splits][B * H_q * N_q][D] fp32
-  float* part_lse;   // [splits][B * H_q * N_q] fp32, base 2
+  float* part_lse;   // [splits][B * H_q * N_q] fp32, base 2, of the weights part_o is
+                     // normalised by (P rounded to the input type): the merge weights
+  float* part_lse_exact;  // the same of the unrounded P (written when lse is requested)
   int64_t part_rows; // B * H_q * N_q
   int32_t splits;
   int32_t split_tiles;
@@ -38,7 +41,8 @@ struct Params {
 // Arguments of the split-KV combine pass: rows are the [B, H_q, N_q] rows of the output.
 struct CombineParams {
   const float* part_o;    // [splits][rows][D]
-  const float* part_lse;  // [splits][rows], base 2
+  const float* part_lse;  // [splits][rows], base 2: merge weights
+  const float* part_lse_exact;  // [splits][rows], base 2: the log-sum-exp output (lse != null)
   uint16_t* o;
   float* lse;             // optional natural-log log-sum-exp [rows]
   int64_t sob, soh, son;

@@ -233,19 +233,19 @@ void attn_fwd_pipe_kernel(const Params p) {
     return grow_any;
   };
   // P = exp2(S * scale - m) (fa2/kernel.py:96-98), rounded to the input type (fa2/kernel.py:105)
+  // bf16: l sums P rounded to bf16, the weights the PV product uses; fp16: the fp32 P (as in
+  // attn_fwd_kernel.hpp, whose header says why)
   auto softmax_p = [&](f32x16 (&s)[MB][NB], u32x4 (&pb)[MB][NT]) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      float rs = 0.f;
+      float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mb][nb][i], qk_scale, -m_i[mb]));
-          s[mb][nb][i] = e;
-          rs += e;
+          s[mb][nb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mb][nb][i], qk_scale, -m_i[mb]));
+          if constexpr (DT == 0) rs0 += s[mb][nb][i];
         }
-      l_i[mb] += rs;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int nb = t >> 1, h = t & 1;
@@ -253,7 +253,14 @@ void attn_fwd_pipe_kernel(const Params p) {
                           E::pack2(s[mb][nb][8 * h + 2], s[mb][nb][8 * h + 3]),
                           E::pack2(s[mb][nb][8 * h + 4], s[mb][nb][8 * h + 5]),
                           E::pack2(s[mb][nb][8 * h + 6], s[mb][nb][8 * h + 7])};
+        if constexpr (DT == 1) {
+          rs0 = E::sum2(pb[mb][t][0], rs0);
+          rs1 = E::sum2(pb[mb][t][1], rs1);
+          rs0 = E::sum2(pb[mb][t][2], rs0);
+          rs1 = E::sum2(pb[mb][t][3], rs1);
+        }
       }
+      l_i[mb] += rs0 + rs1;
     }
   };
   // O^T += V^T P^T for the V tile in `buf` (fa2/kernel.py:100-105)

@@ -81,16 +81,18 @@ int tile_n(int block_n, int head_dim) {
 constexpr int kMaxSplits = 16;
 constexpr int kMinSplitTiles = 4;
 
-// Workspace of a split-KV launch: partial outputs, then partial log-sum-exps, 256-byte aligned.
+// Workspace of a split-KV launch, each part 256-byte aligned: partial outputs, partial
+// log-sum-exps of the rounded P (merge weights), partial exact log-sum-exps (lse output).
 struct WorkspaceLayout {
-  size_t part_o, part_lse, total;
+  size_t part_o, part_lse, part_lse_exact, total;
 };
 WorkspaceLayout workspace_layout(size_t rows, int head_dim, int splits) {
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
   WorkspaceLayout w;
   w.part_o = 0;
   w.part_lse = up((size_t)splits * rows * head_dim * sizeof(float));
-  w.total = w.part_lse + up((size_t)splits * rows * sizeof(float));
+  w.part_lse_exact = w.part_lse + up((size_t)splits * rows * sizeof(float));
+  w.total = w.part_lse_exact + up((size_t)splits * rows * sizeof(float));
   return w;
 }
 
@@ -258,6 +260,7 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
   p.lse = lse;
   p.part_o = nullptr;
   p.part_lse = nullptr;
+  p.part_lse_exact = nullptr;
   p.part_rows = (int64_t)batch * h_q * n_q;
   p.splits = 1;
   p.split_tiles = 0;
@@ -280,6 +283,7 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
       return fail(FA2_EALIGN, "the workspace must be 256-byte aligned");
     p.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.part_o);
     p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.part_lse);
+    p.part_lse_exact = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.part_lse_exact);
     p.splits = splits;
   }
   const int64_t grid = n_tiles * n_bh * splits;
@@ -300,6 +304,7 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
     fa2::CombineParams c;
     c.part_o = p.part_o;
     c.part_lse = p.part_lse;
+    c.part_lse_exact = p.part_lse_exact;
     c.o = p.o;
     c.lse = lse;
     c.sob = p.sob; c.soh = p.soh; c.son = p.son;
