@@ -196,7 +196,7 @@ def test_oracle_on_gpu_matches_oracle_on_cpu():
 
 
 # ------------------------------------------------------------------------------------------
-# the 64-rows-per-wave kernel (block_m 128 / 256 over 32-key tiles, head_dim 64 / 128)
+# 32-key tiles under 128- and 256-row programs (4 and 8 waves)
 # ------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -204,13 +204,13 @@ def test_oracle_on_gpu_matches_oracle_on_cpu():
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("block_m", [128, 256])
 @pytest.mark.parametrize("N", [1, 33, 100, 1000, 2048])
-def test_kernel_r64_family(dtype, causal, D, block_m, N):
+def test_kernel_32_key_tiles(dtype, causal, D, block_m, N):
     q, k, v = make_qkv(BATCH, 16, 4, N, N, D, dtype)
     check_against_oracle(q, k, v, causal, block_m=block_m, block_n=32)
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_kernel_r64_pack_and_lengths(causal):
+def test_kernel_32_key_tiles_pack_and_lengths(causal):
     attention = _attention()
     q, k, v = make_qkv(BATCH, 32, 8, 1000, 1000, 128, torch.bfloat16)
     packed = attention(q, k, v, causal=causal, block_m=128, block_n=32, pack_gqa=True)
@@ -223,6 +223,6 @@ def test_kernel_r64_pack_and_lengths(causal):
 
 
 @pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5"])
-def test_baseline_config_r64(name):
+def test_baseline_config_256_rows_32_keys(name):
     q, k, v, causal = ref.baseline_inputs(name, device="cuda")
     check_against_oracle(q, k, v, causal, precision=torch.float32, block_m=256, block_n=32)

@@ -2,7 +2,6 @@
 // Compiled once per pair with -DFA2_DT=<0 fp16 | 1 bf16> -DFA2_D=<16|32|64|128>.
 #include "attn_fwd_kernel.hpp"
 #include "attn_fwd_launch.hpp"
-#include "attn_fwd_r64.hpp"
 
 #if !defined(FA2_DT) || !defined(FA2_D)
 #error "compile with -DFA2_DT=<0|1> -DFA2_D=<16|32|64|128>"
@@ -44,28 +43,5 @@ int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsign
 }
 
 template int launch_attn_fwd<FA2_DT, FA2_D>(const Params&, int, int, bool, unsigned, hipStream_t);
-
-#if FA2_D >= 64
-namespace {
-template <int DT, int D, int NW>
-int launch_r64_shape(const Params& p, bool causal, unsigned grid, hipStream_t s) {
-  if (causal)
-    hipLaunchKernelGGL((attn_fwd_pipe_kernel<DT, D, NW, 32, true, 2>), dim3(grid), dim3(NW * 64), 0, s, p);
-  else
-    hipLaunchKernelGGL((attn_fwd_pipe_kernel<DT, D, NW, 32, false, 2>), dim3(grid), dim3(NW * 64), 0, s, p);
-  return (int)hipGetLastError();
-}
-}  // namespace
-
-template <int DT, int D>
-int launch_attn_fwd_r64(const Params& p, int waves, int block_n, bool causal, unsigned grid,
-                        hipStream_t s) {
-  (void)block_n;  // 32, checked by the caller
-  return waves == 2 ? launch_r64_shape<DT, D, 2>(p, causal, grid, s)
-                    : launch_r64_shape<DT, D, 4>(p, causal, grid, s);
-}
-
-template int launch_attn_fwd_r64<FA2_DT, FA2_D>(const Params&, int, int, bool, unsigned, hipStream_t);
-#endif
 
 }  // namespace fa2

@@ -16,12 +16,6 @@ template <int DT, int D>
 int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsigned grid,
                     hipStream_t stream);
 
-// Launches attn_fwd_pipe_kernel<DT, D, waves, block_n, causal, 2> (64 query rows per wave);
-// D in {64, 128}, waves in {2, 4}, block_n == 32.
-template <int DT, int D>
-int launch_attn_fwd_r64(const Params& p, int waves, int block_n, bool causal, unsigned grid,
-                        hipStream_t stream);
-
 // Launches the split-KV combine pass (attn_fwd_combine.hip).
 int launch_combine(int dtype, int head_dim, const CombineParams& c, hipStream_t stream);
 
@@ -37,14 +31,5 @@ FA2_DECLARE_LAUNCH(1, 32)
 FA2_DECLARE_LAUNCH(1, 64)
 FA2_DECLARE_LAUNCH(1, 128)
 #undef FA2_DECLARE_LAUNCH
-
-#define FA2_DECLARE_LAUNCH_R64(DT, D)                                                         \
-  extern template int launch_attn_fwd_r64<DT, D>(const Params&, int, int, bool, unsigned, \
-                                                 hipStream_t);
-FA2_DECLARE_LAUNCH_R64(0, 64)
-FA2_DECLARE_LAUNCH_R64(0, 128)
-FA2_DECLARE_LAUNCH_R64(1, 64)
-FA2_DECLARE_LAUNCH_R64(1, 128)
-#undef FA2_DECLARE_LAUNCH_R64
 
 }  // namespace fa2

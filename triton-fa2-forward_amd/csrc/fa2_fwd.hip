@@ -34,16 +34,6 @@ constexpr int kDims[4] = {16, 32, 64, 128};
 constexpr int64_t kMaxRowStride = int64_t(1) << 22;
 
 // Per (dtype, head_dim) launchers, each compiled in its own translation unit.
-int launch_r64(int dtype, int di, const Params& p, int waves, bool causal, unsigned grid,
-               hipStream_t s) {
-  switch (dtype * 4 + di) {
-    case 2: return fa2::launch_attn_fwd_r64<0, 64>(p, waves, 32, causal, grid, s);
-    case 3: return fa2::launch_attn_fwd_r64<0, 128>(p, waves, 32, causal, grid, s);
-    case 6: return fa2::launch_attn_fwd_r64<1, 64>(p, waves, 32, causal, grid, s);
-    default: return fa2::launch_attn_fwd_r64<1, 128>(p, waves, 32, causal, grid, s);
-  }
-}
-
 int launch(int dtype, int di, const Params& p, int waves, int block_n, bool causal, unsigned grid,
            hipStream_t s) {
   switch (dtype * 4 + di) {
@@ -290,14 +280,8 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
   if (grid > 0x7fffffffLL)
     return fail(FA2_EINVAL, "grid of %lld workgroups is too large", (long long)grid);
 
-  // Programs of 128 or 256 rows over 32-key tiles at head_dim 64/128 run the kernel with 64
-  // query rows per wave; everything else, and every launch that writes the log-sum-exp or
-  // splits the key range, the 32-row kernel.
-  const bool r64 = head_dim >= 64 && (block_m == 128 || block_m == 256) && bn == 32 && !lse &&
-                   splits == 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int e = r64 ? launch_r64(dtype, di, p, block_m / 64, causal != 0, (unsigned)grid, st)
-              : launch(dtype, di, p, waves, bn, causal != 0, (unsigned)grid, st);
+  int e = launch(dtype, di, p, waves, bn, causal != 0, (unsigned)grid, st);
   if (e != hipSuccess)
     return fail(FA2_ELAUNCH, "kernel launch failed: %s", hipGetErrorString((hipError_t)e));
   if (splits > 1) {
