@@ -41,7 +41,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams c
   const int64_t b = bh / c.h_q;
   const int head = (int)(bh - b * c.h_q);
   uint16_t* orow = c.o + b * c.sob + head * c.soh + pos * c.son + d0;
-  *(u32x2*)orow = u32x2{E::pack2(o[0] / wsum, o[1] / wsum), E::pack2(o[2] / wsum, o[3] / wsum)};
+  const float inv = 1.0f / wsum;
+  *(u32x2*)orow = u32x2{E::pack2(o[0] * inv, o[1] * inv), E::pack2(o[2] * inv, o[3] * inv)};
   if (c.lse && d0 == 0) {
     float Lx = -INFINITY;
     for (int s = 0; s < c.splits; ++s) Lx = fmaxf(Lx, c.part_lse_exact[s * c.rows + row]);

@@ -361,6 +361,9 @@ void attn_fwd_kernel(const Params p) {
   // ---- normalise once, store once (fa2/kernel.py:178-183)
   const float l = pair_sum(l_i);
   const float lx = want_exact ? pair_sum(l_exact) : l;
+  // one division per row, then multiplies: a per-element fp32 division expands to ~11 VALU
+  // instructions (64 per lane at head_dim 128, ~1.6 us per wave in every program's epilogue)
+  const float inv_l = 1.0f / l;
   if (row_ok) {
     const int64_t row_index = ((int64_t)pr.b * p.h_q + head) * p.n_q + pos;  // in [B, H_q, N_q]
     // log2 of this row's sum of the weights O is normalised by (exp2(s * qk_scale) rounded to
@@ -380,8 +383,8 @@ void attn_fwd_kernel(const Params p) {
             f32x4 lo, hi;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              lo[i] = acc[db][8 * h + i] / l;
-              hi[i] = acc[db][8 * h + 4 + i] / l;
+              lo[i] = acc[db][8 * h + i] * inv_l;
+              hi[i] = acc[db][8 * h + 4 + i] * inv_l;
             }
             *(f32x4*)(po + d0) = lo;
             *(f32x4*)(po + d0 + 4) = hi;
@@ -399,10 +402,10 @@ void attn_fwd_kernel(const Params p) {
         for (int h = 0; h < 2; ++h) {
           const int d0 = 32 * db + 16 * h + 8 * g;
           if (d0 < D) {
-            const u32x4 o = {E::pack2(acc[db][8 * h + 0] / l, acc[db][8 * h + 1] / l),
-                             E::pack2(acc[db][8 * h + 2] / l, acc[db][8 * h + 3] / l),
-                             E::pack2(acc[db][8 * h + 4] / l, acc[db][8 * h + 5] / l),
-                             E::pack2(acc[db][8 * h + 6] / l, acc[db][8 * h + 7] / l)};
+            const u32x4 o = {E::pack2(acc[db][8 * h + 0] * inv_l, acc[db][8 * h + 1] * inv_l),
+                             E::pack2(acc[db][8 * h + 2] * inv_l, acc[db][8 * h + 3] * inv_l),
+                             E::pack2(acc[db][8 * h + 4] * inv_l, acc[db][8 * h + 5] * inv_l),
+                             E::pack2(acc[db][8 * h + 6] * inv_l, acc[db][8 * h + 7] * inv_l)};
             *(u32x4*)(orow + d0) = o;
           }
         }
