@@ -220,7 +220,15 @@ void attn_fwd_kernel(const Params p) {
     issue_k(kv_begin, 0);
     issue_v(kv_begin, 0);
     if (n_tiles_kv > 1) issue_k(kv_begin + BN, 1);
-    wait_vmcnt<0>();
+    // S_0 needs Q and K_0 only: V_0 and K_1 (this wave's last loads; vector loads complete in
+    // order) land while S_0 runs, and the loop's first wait covers them. When the waves issue
+    // unequal numbers of loads, or more than the 6-bit counter holds, wait for all.
+    if constexpr (NI % NW == 0 && 2 * JW < 64) {
+      if (n_tiles_kv > 1) wait_vmcnt<2 * JW>();
+      else wait_vmcnt<JW>();
+    } else {
+      wait_vmcnt<0>();
+    }
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < LA_S; ++ks)
