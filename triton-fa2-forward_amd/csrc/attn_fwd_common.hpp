@@ -162,34 +162,34 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // The workgroup -> (q tile, batch, first query head) decomposition. Workgroups are dealt to
 // the XCDs round-robin; block b runs on XCD b % 8.
-//   * When the (batch, kv head) units split evenly over the XCDs, renumber so that each XCD
-//     receives a contiguous range of "virtual" programs, ordered (batch, kv head) outermost,
-//     then q tile (heaviest causal tile first), then the query-head groups sharing that KV
-//     head: an XCD's L2 then holds the K/V of the heads it is working on (C3: HBM reads
-//     fell from 635 to 139 MiB per launch).
-//   * Otherwise a contiguous range would cut a unit and hand one XCD more of the heavy causal
-//     tiles than another (C5, 12 units over 8 XCDs: 15% more work on XCD 0). Then the order is
-//     q tile outermost, heaviest first, and the round-robin dealing balances the XCDs.
+//   * When the (batch, kv head) units split evenly over the XCDs, each XCD owns a fixed set of
+//     whole units, so its L2 holds the K/V of the heads it works on (C3: HBM reads fell from
+//     635 to 139 MiB per launch). Inside an XCD the order is q tile outermost (heaviest causal
+//     tile first) across all of its units, then unit, then the query-head groups sharing a KV
+//     head. Unit after unit instead started the last unit's heaviest tiles late and left the
+//     XCD's slots 22% idle on C2 (8 units per XCD): the q-tile-major order runs C2 12% faster,
+//     although its L2 now misses more (reads past L2 192 -> ~680 MiB per launch, ~2.6 TB/s).
+//   * Otherwise a fixed unit set per XCD would hand one XCD more of the heavy causal tiles than
+//     another (C5, 12 units over 8 XCDs: 15% more work on XCD 0). Then the order is q tile
+//     outermost over all units, heaviest first, and the round-robin dealing balances the XCDs.
 struct Program {
   int tile, b, hq0, hkv;
 };
 
 template <bool CAUSAL>
 __device__ __forceinline__ Program program_of(const Params& p, int block) {
-  const int total = p.n_tiles * p.n_bh;
   const int progs_per_kv = p.group / p.pack;  // programs sharing one KV head per q tile
   const int h_kv = p.h_q / p.group;
   const int units = p.n_bh / progs_per_kv;    // batch * h_kv
   int kv_index, t, h_in;
   if (units % kXcds == 0) {
-    const int q = total / kXcds, rem = total % kXcds;
     const int xcd = block % kXcds, slot = block / kXcds;
-    const int v = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + slot;
-    const int per_kv = p.n_tiles * progs_per_kv;
-    kv_index = v / per_kv;                    // b * h_kv + hkv
-    const int r = v - kv_index * per_kv;
-    t = r / progs_per_kv;
-    h_in = r - t * progs_per_kv;
+    const int upx = units / kXcds;             // units per XCD
+    const int per_t = upx * progs_per_kv;      // programs per q tile on one XCD
+    t = slot / per_t;
+    const int r = slot - t * per_t;
+    kv_index = xcd * upx + r / progs_per_kv;   // b * h_kv + hkv
+    h_in = r % progs_per_kv;
   } else {
     t = block / p.n_bh;
     const int r = block - t * p.n_bh;
