@@ -25,8 +25,8 @@
 //     4-key x 16-dim block and every lane receives 4 consecutive keys of one dim.
 //   * O^T accumulates in 32x32 blocks whose lane l holds column l%32 = the lane's own
 //     query row, so the per-row rescale by alpha is a lane-local multiply.
-//   * K/V tiles go HBM -> LDS directly (buffer_load_dwordx4 ... lds, no VGPR staging) into a
-//     double buffer: tile j+1 is in flight while tile j is consumed; one barrier per tile.
+//   * K/V tiles go HBM -> LDS directly (buffer_load_dwordx4 ... lds, no VGPR staging) into
+//     double buffers, K two tiles and V one tile ahead of their product; one barrier per tile.
 //   * LDS layouts are XOR-swizzled at 16-byte granularity so that both the b128 reads
 //     of K and the transposing b64 reads of V are free of bank conflicts; the swizzle is
 //     applied by choosing which global chunk each lane fetches.
@@ -274,9 +274,9 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
     for (int i = 0; i < LA_V; ++i) va[i] = v_operand(buf, i / DB, i % DB);
 
-    // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos.
-    // `masked` is uniform over the workgroup; one copy of the tile code serves both cases
-    // so the accumulators keep one register assignment across the loop.
+    // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos. The
+    // condition is uniform over the workgroup (a scalar branch), and one copy of the tile code
+    // serves masked and unmasked tiles so the accumulators keep one register assignment.
     if (n0 + BN > full_end) {
       const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
 #pragma unroll
