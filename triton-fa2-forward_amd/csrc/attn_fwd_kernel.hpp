@@ -192,9 +192,11 @@ void attn_fwd_kernel(const Params p) {
   // convex combination of V rows. With the lazy reference max a row's largest P is 2^x, not 1,
   // and its bf16 rounding (2^-9) would otherwise reach a row dominated by one key in full
   // (C5's outlier keys: 1.74x SDPA's error with the fp32 sum, 0.93x with this one). l_exact then
-  // sums the unrounded P for the log-sum-exp output. fp16 rounds P 8x finer: l sums the fp32 P
-  // there, as the reference does (fa2/kernel.py:98), and is itself the exact sum.
-  constexpr bool kRoundedSum = DT == 1;
+  // sums the unrounded P for the log-sum-exp output. fp16 rounds P 8x finer, so either sum is
+  // accurate there; the rounded one (v_dot2, half the instructions) is faster at head_dim 128
+  // (+2.5% on C3's shape) and the fp32 one, as in the reference (fa2/kernel.py:98), at 64 and
+  // below (C4: 3.4% faster).
+  constexpr bool kRoundedSum = DT == 1 || D == 128;
   float m_i = -INFINITY;
   float l_i = 0.f;
   float l_exact = 0.f;
