@@ -85,6 +85,34 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
                     int32_t block_m, int32_t block_n, float qk_scale, float* lse,
                     int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Variant bits of fa2_attn_fwd_variant. */
+#define FA2_VARIANT_SCALE_FIRST 1      /* bench/ablation.py:13-14, "scale_first"     */
+#define FA2_VARIANT_MASK_EVERY_TILE 2  /* bench/ablation.py:15, "mask_every_tile"    */
+
+/*
+ * fa2_attn_fwd_variant - the forward kernel with the reference's two non-skipping ablation
+ * switches, for timing the design choices they undo. Counterpart of `attention_ablate`'s
+ * scale_first / mask_every_tile (bench/ablation.py:11-17, 182-200), which launch a copy of
+ * `_attn_fwd`; here the switches are compile-time flags of the one kernel template.
+ *
+ *   variant  0, or an OR of FA2_VARIANT_SCALE_FIRST (multiply every score by the scale, then
+ *            subtract the row max: two instructions per score instead of one FMA) and
+ *            FA2_VARIANT_MASK_EVERY_TILE (apply the causal / end-of-sequence mask on every K/V
+ *            tile, not only on the tiles that need it). 0 runs the production kernel.
+ *
+ * Every variant computes the same attention: MASK_EVERY_TILE bit for bit, SCALE_FIRST to fp32
+ * rounding of the exponent. Runs at the default configuration (block_m 128,
+ * fa2_default_config's block_n), without split-KV or log-sum-exp; the other arguments are
+ * those of fa2_attn_fwd. The reference's skipping switches (no_exp, no_softmax, kv_l2) make
+ * wrong outputs by design and have no entry point.
+ */
+int fa2_attn_fwd_variant(const void* q, const void* k, const void* v, void* out,
+                         const int64_t q_stride[4], const int64_t k_stride[4],
+                         const int64_t v_stride[4], const int64_t o_stride[4],
+                         int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                         int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                         float qk_scale, int32_t variant, void* stream);
+
 /*
  * fa2_workspace_bytes - workspace size of a split-KV launch of fa2_attn_fwd_ex: fp32 partial
  * outputs and log-sum-exps of every split. 0 when num_splits <= 1 or a size is not positive.

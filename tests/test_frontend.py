@@ -245,6 +245,38 @@ def test_workspace_bytes():
     assert lib.fa2_workspace_bytes(16, 32, 0, 128, 4) == 0
 
 
+# ------------------------------------------------------------------------------------------
+# fa2_attn_fwd_variant / attention_ablate: the timing variants (reference bench/ablation.py)
+# ------------------------------------------------------------------------------------------
+
+@needs_lib
+def test_c_abi_variant_rejects_unknown_bits():
+    arr = lambda s: (ctypes.c_int64 * 4)(*s)  # noqa: E731
+    lib = _lib.lib()
+    st = arr((8192, 2048, 64, 1))
+    for bad in (4, 8, -1):
+        rc = lib.fa2_attn_fwd_variant(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
+                                      32, 64, 0, 1, 1, 0.18, bad, None)
+        assert rc == -1 and "variant" in _lib.last_error(), (bad, rc)
+    # the shared argument checks apply to every variant
+    rc = lib.fa2_attn_fwd_variant(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
+                                  32, 48, 0, 1, 1, 0.18, 1, None)
+    assert rc == -1 and "head_dim" in _lib.last_error()
+
+
+def test_ablation_skipping_switches_are_not_built():
+    from ablation import SKIPPING, attention_ablate
+
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
+    for knob in SKIPPING:
+        with pytest.raises(ValueError, match="skip work"):
+            attention_ablate(q, q, q, **{knob: True})
+    with pytest.raises(AssertionError, match="unknown"):
+        attention_ablate(q, q, q, fast=True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        attention_ablate(q, q, q, scale_first=True)
+
+
 def test_split_and_lse_arguments_fail_in_python():
     q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
     with pytest.raises(ValueError, match="num_splits"):

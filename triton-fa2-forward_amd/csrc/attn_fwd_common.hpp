@@ -29,6 +29,9 @@ constexpr int kXcds = 8;
 constexpr float kRescaleTau = 8.0f;
 // ln 2: a base-2 log-sum-exp times this is the natural one
 constexpr float kLn2 = 0.6931471805599453f;
+// Kernel variant bits (attn_fwd_kernel's VARIANT; FA2_VARIANT_* in the C ABI)
+constexpr int kVariantScaleFirst = 1;
+constexpr int kVariantMaskEveryTile = 2;
 
 // ---------------------------------------------------------------------------------
 // element type traits: the MFMA, the fp32 -> 16-bit pair conversion (RNE) and the fp32 sum of

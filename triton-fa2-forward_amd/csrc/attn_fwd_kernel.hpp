@@ -44,10 +44,17 @@ namespace fa2 {
 // ---------------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------------
-template <int DT, int D, int NW, int BN, bool CAUSAL>
+// VARIANT is 0 for the product. Its bits turn on the two instruction-count choices the
+// reference's ablation undoes (bench/ablation.py:11-17), for timing them against the product:
+// kVariantScaleFirst scales every score before the row max and subtracts the max separately
+// (two VALU instructions per score instead of one FMA); kVariantMaskEveryTile applies the mask
+// on every K/V tile, not only on the tiles that need it. Both compute the same attention.
+template <int DT, int D, int NW, int BN, bool CAUSAL, int VARIANT = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_kernel(const Params p) {
   using E = Elem<DT>;
+  constexpr bool kScaleFirst = (VARIANT & kVariantScaleFirst) != 0;
+  constexpr bool kMaskEveryTile = (VARIANT & kVariantMaskEveryTile) != 0;
   constexpr int KS = D / 16;               // 16-dim k-steps of S^T = K Q^T
   constexpr int DB = (D + 31) / 32;        // 32-dim row blocks of O^T
   constexpr int NB = BN / 32;              // 32-key row blocks of S^T
@@ -279,7 +286,7 @@ void attn_fwd_kernel(const Params p) {
     // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos. The
     // condition is uniform over the workgroup (a scalar branch), and one copy of the tile code
     // serves masked and unmasked tiles so the accumulators keep one register assignment.
-    if (n0 + BN > full_end) {
+    if (kMaskEveryTile || n0 + BN > full_end) {
       const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -288,12 +295,16 @@ void attn_fwd_kernel(const Params p) {
           if (nb * 32 + 16 * (i / 8) + (i % 8) > lim) s[nb][i] = -INFINITY;
     }
     // online softmax in base 2 (fa2/kernel.py:95-98), with a lazily moved reference max
+    if constexpr (kScaleFirst) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s[nb] *= qk_scale;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
-    mx = pair_max(mx) * qk_scale;
+    mx = kScaleFirst ? pair_max(mx) : pair_max(mx) * qk_scale;
     const bool grow = mx > m_i + kRescaleTau;
     if (__builtin_amdgcn_ballot_w64(grow)) {
       const float m_new = grow ? mx : m_i;
@@ -308,7 +319,8 @@ void attn_fwd_kernel(const Params p) {
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        s[nb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][i], qk_scale, -m_i));
+        s[nb][i] = __builtin_amdgcn_exp2f(kScaleFirst ? s[nb][i] - m_i
+                                                      : __builtin_fmaf(s[nb][i], qk_scale, -m_i));
     if constexpr (!kRoundedSum) {
       float rs = 0.f;
 #pragma unroll

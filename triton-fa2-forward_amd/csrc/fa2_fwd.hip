@@ -48,6 +48,21 @@ int launch(int dtype, int di, const Params& p, int waves, int block_n, bool caus
   }
 }
 
+// The timing variants (attn_fwd_kernel's VARIANT), at 4 waves and the default K/V tile.
+int launch_variant(int dtype, int di, const Params& p, int variant, bool causal, unsigned grid,
+                   hipStream_t s) {
+  switch (dtype * 4 + di) {
+    case 0: return fa2::launch_attn_fwd_variant<0, 16>(p, variant, causal, grid, s);
+    case 1: return fa2::launch_attn_fwd_variant<0, 32>(p, variant, causal, grid, s);
+    case 2: return fa2::launch_attn_fwd_variant<0, 64>(p, variant, causal, grid, s);
+    case 3: return fa2::launch_attn_fwd_variant<0, 128>(p, variant, causal, grid, s);
+    case 4: return fa2::launch_attn_fwd_variant<1, 16>(p, variant, causal, grid, s);
+    case 5: return fa2::launch_attn_fwd_variant<1, 32>(p, variant, causal, grid, s);
+    case 6: return fa2::launch_attn_fwd_variant<1, 64>(p, variant, causal, grid, s);
+    default: return fa2::launch_attn_fwd_variant<1, 128>(p, variant, causal, grid, s);
+  }
+}
+
 int dim_index(int d) {
   for (int i = 0; i < 4; ++i)
     if (kDims[i] == d) return i;
@@ -56,9 +71,7 @@ int dim_index(int d) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// gfx950 default K/V tile (sweep.py on the BASELINE.json configs, MI355X): 64 keys at
-// head_dim 128 (C2, C3, C5 best), 128 keys at head_dim 64 (C4: 900 vs 857 TFLOP/s).
-int default_block_n(int head_dim) { return head_dim == 64 ? 128 : 64; }
+using fa2::default_block_n;
 
 // block_n request -> the K/V tile width the kernels are built for (0 = the default)
 int tile_n(int block_n, int head_dim) {
@@ -85,6 +98,14 @@ WorkspaceLayout workspace_layout(size_t rows, int head_dim, int splits) {
   w.total = w.part_lse_exact + up((size_t)splits * rows * sizeof(float));
   return w;
 }
+
+int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
+                  const int64_t q_stride[4], const int64_t k_stride[4],
+                  const int64_t v_stride[4], const int64_t o_stride[4], int32_t batch,
+                  int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                  int32_t dtype, int32_t causal, int32_t pack, int32_t block_m, int32_t block_n,
+                  float qk_scale, float* lse, int32_t num_splits, void* workspace,
+                  size_t workspace_bytes, int32_t variant, void* stream);
 
 }  // namespace
 
@@ -164,6 +185,37 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
                     int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
                     int32_t block_m, int32_t block_n, float qk_scale, float* lse,
                     int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream) {
+  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                       n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale, lse,
+                       num_splits, workspace, workspace_bytes, 0, stream);
+}
+
+int fa2_attn_fwd_variant(const void* q, const void* k, const void* v, void* out,
+                         const int64_t q_stride[4], const int64_t k_stride[4],
+                         const int64_t v_stride[4], const int64_t o_stride[4],
+                         int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                         int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                         float qk_scale, int32_t variant, void* stream) {
+  if (variant & ~(FA2_VARIANT_SCALE_FIRST | FA2_VARIANT_MASK_EVERY_TILE)) {
+    g_err[0] = '\0';
+    return fail(FA2_EINVAL, "unknown variant bits 0x%x", (unsigned)variant);
+  }
+  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                       n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
+                       nullptr, 0, variant, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
+                  const int64_t q_stride[4], const int64_t k_stride[4],
+                  const int64_t v_stride[4], const int64_t o_stride[4], int32_t batch,
+                  int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                  int32_t dtype, int32_t causal, int32_t pack, int32_t block_m, int32_t block_n,
+                  float qk_scale, float* lse, int32_t num_splits, void* workspace,
+                  size_t workspace_bytes, int32_t variant, void* stream) {
   g_err[0] = '\0';
   // ---- shape checks (fa2/kernel.py:218-228)
   if (batch < 0 || h_q <= 0 || h_kv <= 0 || n_q < 0 || n_kv < 0)
@@ -281,7 +333,8 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
     return fail(FA2_EINVAL, "grid of %lld workgroups is too large", (long long)grid);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int e = launch(dtype, di, p, waves, bn, causal != 0, (unsigned)grid, st);
+  int e = variant ? launch_variant(dtype, di, p, variant, causal != 0, (unsigned)grid, st)
+                  : launch(dtype, di, p, waves, bn, causal != 0, (unsigned)grid, st);
   if (e != hipSuccess)
     return fail(FA2_ELAUNCH, "kernel launch failed: %s", hipGetErrorString((hipError_t)e));
   if (splits > 1) {
@@ -303,4 +356,4 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
   return FA2_OK;
 }
 
-}  // extern "C"
+}  // namespace
