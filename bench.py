@@ -14,10 +14,14 @@ Protocol (the reference's, bench/bench.py:51-92, restated for ROCm):
   * an untimed settle phase (steps back to back for 1 s: the GPU's clocks ramp up over the
     first few dozen launches after the idle gate, and each process sees one 17-25 ms hold-up
     in its first half second of GPU work; reported as "settle"), then W untimed
-    warmups, then exactly K (default 100) back-to-back steps bracketed by synchronize; `value`
-    is K x FLOPs / that wall time; FLOPs = 4 B H_q pairs D with causal pairs N(N+1)/2;
-  * HIP events around every launch on the launch stream give the kernel's average duration
-    (roofline.achieved) and the median / IQR;
+    warmups, then exactly K (default 100) back-to-back steps bracketed by synchronize and by
+    one pair of HIP events on the launch stream; `value` is K x FLOPs / the events' elapsed
+    time, and that time / K is the kernel's average launch duration (roofline.achieved);
+    FLOPs = 4 B H_q pairs D with causal pairs N(N+1)/2. No event sits between the timed steps:
+    a timed event between two launches adds a few microseconds of GPU-side gap (6.5 us per
+    step on C3, 1.3%; 6 us on C5's 35 us kernel);
+  * a second pass of K steps with events around every launch, the reference's own protocol,
+    gives the median / IQR and the slowest steps (these per-launch times include that gap);
   * a second pass follows the reference's flush protocol exactly: a 1 GiB fill (larger than
     L2 + the 256 MB Infinity Cache) before every iteration, median of per-iteration events;
   * cpu_baseline: the oracle's blocked_attention (the reference's CPU path, fa2/reference.py:
@@ -130,27 +134,41 @@ def settle_clocks(fn, min_ms=1000.0, max_steps=20000):
 
 
 def time_steps(fn, steps, warmup):
+    """W untimed warmups, then `steps` back-to-back launches between one pair of HIP events
+    on the launch stream, synchronized on both sides. Returns (elapsed ms of the events, host
+    wall ms of the timed loop including the final synchronize)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     begin, finish = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     begin.record(stream)
+    for _ in range(steps):
+        fn()
+    finish.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    return begin.elapsed_time(finish), wall_ms
+
+
+def time_each(fn, steps):
+    """The reference's per-iteration protocol (bench/bench.py:61-80): events around every
+    launch; returns the per-launch ms (each includes the gap a timed event adds)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
     for s, e in zip(starts, ends):
         s.record(stream)
         fn()
         e.record(stream)
-    finish.record(stream)
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return per, begin.elapsed_time(finish), wall_ms
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
 def flushed_median(fn, iters):
@@ -259,8 +277,9 @@ def run(name, steps, warmup, with_cpu, flush_iters):
         raise SystemExit(f"correctness gate failed on {name}: max-abs vs SDPA {err:.3e}")
 
     settle = settle_clocks(fn)
-    per, total_ms, wall_ms = time_steps(fn, steps, warmup)
-    avg_kernel_ms = sum(per) / len(per)
+    total_ms, wall_ms = time_steps(fn, steps, warmup)
+    avg_kernel_ms = total_ms / steps   # one kernel launch per step
+    per = time_each(fn, steps)
     q1, med, q3 = statistics.quantiles(per, n=4, method="inclusive") if len(per) > 1 else (per[0],) * 3
     value = flops * steps / (total_ms * 1e-3) / 1e12
     achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
@@ -290,8 +309,9 @@ def run(name, steps, warmup, with_cpu, flush_iters):
                      "traffic_source": traffic["source"] if traffic else None,
                      "algorithmic_bytes": min_bytes,
                      "kernel": "fa2::attn_fwd_kernel", "avg_kernel_ms": round(avg_kernel_ms, 5)},
-        "median_ms": round(med, 5), "p25_ms": round(q1, 5), "p75_ms": round(q3, 5),
-        "slowest_steps": [[i, round(per[i], 4)] for i in sorted(range(len(per)), key=per.__getitem__)[-3:]],
+        "per_launch_events": {"median_ms": round(med, 5), "p25_ms": round(q1, 5), "p75_ms": round(q3, 5),
+                              "slowest_steps": [[i, round(per[i], 4)] for i in
+                                                sorted(range(len(per)), key=per.__getitem__)[-3:]]},
         "host_wall_ms": round(wall_ms, 3),
         "vs_reference_h100_c3": round(value / H100_C3_TFLOPS, 3) if name == "C3" else None,
         "correctness_gate": {"max_abs_vs_sdpa": err, "sdpa_backend": backend},
@@ -316,7 +336,7 @@ HBM_PEAK_GBS = 8000.0
 
 
 def run_pack_short(n_q, steps, warmup):
-    """One line of the few-queries regime: median kernel time and the K/V read rate
+    """One line of the few-queries regime: time per step (back to back) and the K/V read rate
     (bench/bench.py:90-92: bytes of K and V over the time, the bound when N_q is small)."""
     import torch
 
@@ -335,10 +355,11 @@ def run_pack_short(n_q, steps, warmup):
     if err is not None and not (math.isfinite(err) and err <= 2e-2):
         raise SystemExit(f"correctness gate failed on pack-short N_q={n_q}: max-abs vs SDPA {err:.3e}")
     settle = settle_clocks(fn)
-    per, total_ms, _ = time_steps(fn, steps, warmup)
-    med = statistics.median(per)
+    total_ms, _ = time_steps(fn, steps, warmup)
+    step_ms = total_ms / steps          # one step: the attention launch (and the merge, if split)
+    med = statistics.median(time_each(fn, steps))
     kv = 2 * k.numel() * k.element_size()
-    rate_gbs = kv / (med * 1e-3) / 1e9
+    rate_gbs = kv / (step_ms * 1e-3) / 1e9
     splits = _lib.num_splits(c["B"], c["H_q"], c["H_kv"], n_q, c["N_kv"], c["D"], False, 128, 64,
                              _cu_count(q.device))
     return {
@@ -350,9 +371,10 @@ def run_pack_short(n_q, steps, warmup):
                                f"N_q={n_q} N_kv={c['N_kv']} D={c['D']}",
                    "n_q": n_q, "pack_gqa": should_pack_gqa(n_q, c["H_q"] // c["H_kv"], 128),
                    "num_splits": splits},
-        "median_us": round(med * 1e3, 2),
+        "us_per_step": round(step_ms * 1e3, 2),
+        "per_launch_events_median_us": round(med * 1e3, 2),
         "reference_h100_us": PACK_SHORT_H100_US.get(n_q),
-        "vs_reference_h100": (round(PACK_SHORT_H100_US[n_q] / (med * 1e3), 3)
+        "vs_reference_h100": (round(PACK_SHORT_H100_US[n_q] / (step_ms * 1e3), 3)
                               if n_q in PACK_SHORT_H100_US else None),
         "roofline": {"bound": "hbm", "achieved": round(rate_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(rate_gbs / HBM_PEAK_GBS, 4), "traffic": None,

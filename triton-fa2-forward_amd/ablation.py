@@ -19,8 +19,9 @@ tests/test_gpu_ablation.py checks); pack forces GQA head packing. The reference'
 switches (no_exp, no_softmax, kv_l2) skip work and produce wrong outputs by design. They are not
 part of this library: their numbers come from a separate, unshipped copy of the kernel.
 
-Timing follows bench.py (1 s clock settle, then per-step HIP events), interleaved over rounds so
-that clock drift hits every variant alike (bench/ablation.py:252-255).
+Timing follows the reference (HIP events around every launch, median and IQR) after bench.py's
+1 s clock settle, interleaved over rounds so that clock drift hits every variant alike
+(bench/ablation.py:252-255).
 """
 
 import argparse
@@ -136,8 +137,9 @@ def main():
         samples = {name: [] for name in fns}
         for _ in range(args.rounds):
             for name, fn in fns.items():
-                per, _, _ = bench.time_steps(fn, args.iters, args.warmup)
-                samples[name] += per
+                for _ in range(args.warmup):
+                    fn()
+                samples[name] += bench.time_each(fn, args.iters)
         base = _summarize(samples["production"])
         print(f"\nN={N} {args.dtype} H {args.hq}/{args.hkv} D {args.head_dim} causal  "
               f"(production {base['median_ms']:.3f} ms, {flops / base['median_ms'] / 1e9:.1f} TFLOP/s)")
