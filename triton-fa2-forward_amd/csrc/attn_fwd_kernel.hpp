@@ -244,7 +244,16 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand_v(0, ks, nb);
   }
-  for (int j = 0; j < n_tiles_kv; ++j) {
+  // Causal: the last tiles of a program can start past every row of a wave (the second masked
+  // tile of a 128-row program, for its first 64 rows). The wave skips their products and
+  // softmax, which would add exact zeros, and keeps only its share of the loads and barriers
+  // (the loop after this one). Measured +0.2% on C3, +0.5% on C2, +1.9% on C5.
+  int n_active = n_tiles_kv;
+  if (CAUSAL) {
+    const int wave_last = __builtin_amdgcn_readlane(pos_vis, 31);  // rows grow with the lane
+    if (wave_last < kv_end) n_active = min(n_tiles_kv, (wave_last - kv_begin) / BN + 1);
+  }
+  for (int j = 0; j < n_active; ++j) {
     const int n0 = kv_begin + j * BN;
     const int buf = j & 1;
 
@@ -378,6 +387,13 @@ void attn_fwd_kernel(const Params p) {
     }
   }
 
+  for (int j = n_active; j < n_tiles_kv; ++j) {
+    const int n0 = kv_begin + j * BN;
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, j & 1);
+    if (j + 1 < n_tiles_kv) issue_v(n0 + BN, (j & 1) ^ 1);
+  }
   __builtin_amdgcn_s_setprio(0);
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
