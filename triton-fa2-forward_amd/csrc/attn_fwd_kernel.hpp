@@ -35,6 +35,9 @@
 //     on most tiles. The result is the same softmax: acc and l share the reference.
 //   * Programs are ordered so that each XCD (its own L2) works through whole KV heads,
 //     heaviest causal tiles first.
+//   * At head_dim 64 the tile loop is software-pipelined inside each wave (S_{j+1}'s MFMAs
+//     next to softmax_j, PV_j's next to the row max of S_{j+1}): there a tile's softmax needs
+//     more issue time than its MFMAs. At 128 the waves of a SIMD overlap each other instead.
 #pragma once
 
 #include "attn_fwd_common.hpp"
@@ -74,7 +77,8 @@ void attn_fwd_kernel(const Params p) {
 
   // split-KV: consecutive workgroups are the splits of one program
   const int split = p.splits > 1 ? (int)blockIdx.x % p.splits : 0;
-  const Program pr = program_of<CAUSAL>(p, p.splits > 1 ? (int)blockIdx.x / p.splits : (int)blockIdx.x);
+  const Program pr =
+      program_of<CAUSAL>(p, p.splits > 1 ? (int)blockIdx.x / p.splits : (int)blockIdx.x);
 
   // ---- this lane's query row: packed row r -> (position r / pack, head r % pack)
   // (fa2/kernel.py:135-139). Rows past block_m or past n_q compute on zeros and are
@@ -213,188 +217,428 @@ void attn_fwd_kernel(const Params p) {
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
   const float qk_scale = p.qk_scale;
 
-  // ---- main loop. Per tile j, one barrier, placed between the two products:
-  //   S_j = K_j Q^T                      K_j's operands partly read during PV_{j-1}
-  //   wait + barrier                     V_j and K_{j+1} have landed; every wave is past S_j
-  //   issue K_{j+2} -> K buffer of K_j, V_{j+1} -> V buffer of V_{j-1}
-  //   read the first V_j operands, then mask + softmax_j while they arrive
-  //   O += V_j P_j, with V_j operands read LA_V MFMAs ahead and K_{j+1}'s first operands
-  //   read in between, so every LDS read has MFMA time to land in.
-  constexpr int LA_S = KS < 4 ? KS : 4;        // k-steps of K operands read ahead
-  constexpr int NPV = (BN / 16) * DB;          // MFMAs of the PV product
-  constexpr int LA_V = NPV < 4 ? NPV : 4;      // PV MFMAs whose V operands are read ahead
-  constexpr int NKP = LA_S * NB;               // K operand reads prefetched during PV
-  u32x4 kop[LA_S][NB];
-  if (n_tiles_kv > 0) {
-    issue_k(kv_begin, 0);
-    issue_v(kv_begin, 0);
-    if (n_tiles_kv > 1) issue_k(kv_begin + BN, 1);
-    // S_0 needs Q and K_0 only: V_0 and K_1 (this wave's last loads; vector loads complete in
-    // order) land while S_0 runs, and the loop's first wait covers them. When the waves issue
-    // unequal numbers of loads, or more than the 6-bit counter holds, wait for all.
-    if constexpr (NI % NW == 0 && 2 * JW < 64) {
-      if (n_tiles_kv > 1) wait_vmcnt<2 * JW>();
-      else wait_vmcnt<JW>();
-    } else {
-      wait_vmcnt<0>();
+  // The main loop: at head_dim 64 software-pipelined across tiles inside each wave, else
+  // one tile at a time with two waves per SIMD overlapping each other (measured per D). The
+  // pipelined loop holds two S tiles: at 128-key tiles that spills, so those keep the other.
+  constexpr bool kPipelined = D == 64 && BN <= 64;
+  if constexpr (!kPipelined) {
+    // ---- main loop. Per tile j, one barrier, placed between the two products:
+    //   S_j = K_j Q^T                      K_j's operands partly read during PV_{j-1}
+    //   wait + barrier                     V_j and K_{j+1} have landed; every wave is past S_j
+    //   issue K_{j+2} -> K buffer of K_j, V_{j+1} -> V buffer of V_{j-1}
+    //   read the first V_j operands, then mask + softmax_j while they arrive
+    //   O += V_j P_j, with V_j operands read LA_V MFMAs ahead and K_{j+1}'s first operands
+    //   read in between, so every LDS read has MFMA time to land in.
+    constexpr int LA_S = KS < 4 ? KS : 4;        // k-steps of K operands read ahead
+    constexpr int NPV = (BN / 16) * DB;          // MFMAs of the PV product
+    constexpr int LA_V = NPV < 4 ? NPV : 4;      // PV MFMAs whose V operands are read ahead
+    constexpr int NKP = LA_S * NB;               // K operand reads prefetched during PV
+    u32x4 kop[LA_S][NB];
+    if (n_tiles_kv > 0) {
+      issue_k(kv_begin, 0);
+      issue_v(kv_begin, 0);
+      if (n_tiles_kv > 1) issue_k(kv_begin + BN, 1);
+      // S_0 needs Q and K_0 only: V_0 and K_1 (this wave's last loads; vector loads complete in
+      // order) land while S_0 runs, and the loop's first wait covers them. When the waves issue
+      // unequal numbers of loads, or more than the 6-bit counter holds, wait for all.
+      if constexpr (NI % NW == 0 && 2 * JW < 64) {
+        if (n_tiles_kv > 1) wait_vmcnt<2 * JW>();
+        else wait_vmcnt<JW>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < LA_S; ++ks)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand_v(0, ks, nb);
     }
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < LA_S; ++ks)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand_v(0, ks, nb);
-  }
-  // Causal: the last tiles of a program can start past every row of a wave (the second masked
-  // tile of a 128-row program, for its first 64 rows). The wave skips their products and
-  // softmax, which would add exact zeros, and keeps only its share of the loads and barriers
-  // (the loop after this one). Measured +0.2% on C3, +0.5% on C2, +1.9% on C5.
-  int n_active = n_tiles_kv;
-  if (CAUSAL) {
-    const int wave_last = __builtin_amdgcn_readlane(pos_vis, 31);  // rows grow with the lane
-    if (wave_last < kv_end) n_active = min(n_tiles_kv, (wave_last - kv_begin) / BN + 1);
-  }
-  for (int j = 0; j < n_active; ++j) {
-    const int n0 = kv_begin + j * BN;
-    const int buf = j & 1;
+    // Causal: the last tiles of a program can start past every row of a wave (the second masked
+    // tile of a 128-row program, for its first 64 rows). The wave skips their products and
+    // softmax, which would add exact zeros, and keeps only its share of the loads and barriers
+    // (the loop after this one). Measured +0.2% on C3, +0.5% on C2, +1.9% on C5.
+    int n_active = n_tiles_kv;
+    if (CAUSAL) {
+      const int wave_last = __builtin_amdgcn_readlane(pos_vis, 31);  // rows grow with the lane
+      if (wave_last < kv_end) n_active = min(n_tiles_kv, (wave_last - kv_begin) / BN + 1);
+    }
+    for (int j = 0; j < n_active; ++j) {
+      const int n0 = kv_begin + j * BN;
+      const int buf = j & 1;
 
-    // S^T = K Q^T  (fa2/kernel.py:75-79). The two products run at raised wave priority and
-    // the softmax at the base one, so that when the two waves of a SIMD meet, the one with
-    // matrix work issues first and the other's softmax fills the issue slots the MFMAs leave
-    // (3% on MI355X over equal priorities; raising it for only one of the products gains nothing).
-    __builtin_amdgcn_s_setprio(1);
-    f32x16 s[NB];
+      // S^T = K Q^T  (fa2/kernel.py:75-79). The two products run at raised wave priority and
+      // the softmax at the base one, so that when the two waves of a SIMD meet, the one with
+      // matrix work issues first and the other's softmax fills the issue slots the MFMAs leave
+      // (3% on MI355X over equal priorities; raising it for only one product gains nothing).
+      __builtin_amdgcn_s_setprio(1);
+      f32x16 s[NB];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) s[nb] = f32x16{};
+      for (int nb = 0; nb < NB; ++nb) s[nb] = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int slot = ks % LA_S;
+      for (int ks = 0; ks < KS; ++ks) {
+        const int slot = ks % LA_S;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) s[nb] = E::mma(kop[slot][nb], qreg[ks], s[nb]);
-      if (ks + LA_S < KS) {
+        for (int nb = 0; nb < NB; ++nb) s[nb] = E::mma(kop[slot][nb], qreg[ks], s[nb]);
+        if (ks + LA_S < KS) {
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) kop[slot][nb] = k_operand(buf, ks + LA_S, nb);
+          for (int nb = 0; nb < NB; ++nb) kop[slot][nb] = k_operand(buf, ks + LA_S, nb);
+        }
+      }
+      // keep the K reads LA_S k-steps ahead of the MFMAs that consume them
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
+        if (ks + LA_S < KS) __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
+      }
+
+      __builtin_amdgcn_s_setprio(0);
+      wait_vmcnt<0>();  // this wave's loads of V_j and K_{j+1} have landed
+      __syncthreads();                // ... every wave's; and every wave is done with K_j
+      if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, buf);
+      if (j + 1 < n_tiles_kv) issue_v(n0 + BN, buf ^ 1);
+
+      u32x4 va[LA_V];
+#pragma unroll
+      for (int i = 0; i < LA_V; ++i) va[i] = v_operand(buf, i / DB, i % DB);
+
+      // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos. The
+      // condition is uniform over the workgroup (a scalar branch), and one copy of the tile code
+      // serves masked and unmasked tiles so the accumulators keep one register assignment.
+      if (kMaskEveryTile || n0 + BN > full_end) {
+        const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (nb * 32 + 16 * (i / 8) + (i % 8) > lim) s[nb][i] = -INFINITY;
+      }
+      // online softmax in base 2 (fa2/kernel.py:95-98), with a lazily moved reference max
+      if constexpr (kScaleFirst) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) s[nb] *= qk_scale;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
+      mx = kScaleFirst ? pair_max(mx) : pair_max(mx) * qk_scale;
+      const bool grow = mx > m_i + kRescaleTau;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float m_new = grow ? mx : m_i;
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+        l_i *= alpha;
+        l_exact *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+        m_i = m_new;
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          s[nb][i] = __builtin_amdgcn_exp2f(kScaleFirst ? s[nb][i] - m_i
+                                                        : __builtin_fmaf(s[nb][i], qk_scale, -m_i));
+      if constexpr (!kRoundedSum) {
+        float rs = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) rs += s[nb][i];
+        l_i += rs;
+      } else if (want_exact) {
+        float rx = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) rx += s[nb][i];
+        l_exact += rx;
+      }
+
+      // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
+      u32x4 pb[BN / 16];
+#pragma unroll
+      for (int t = 0; t < BN / 16; ++t) {
+        const int nb = t >> 1, h = t & 1;
+        pb[t] = u32x4{E::pack2(s[nb][8 * h + 0], s[nb][8 * h + 1]),
+                      E::pack2(s[nb][8 * h + 2], s[nb][8 * h + 3]),
+                      E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
+                      E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
+      }
+      if constexpr (kRoundedSum) {
+        float rs0 = 0.f, rs1 = 0.f;
+#pragma unroll
+        for (int t = 0; t < BN / 16; ++t) {
+          rs0 = E::sum2(pb[t][0], rs0);
+          rs1 = E::sum2(pb[t][1], rs1);
+          rs0 = E::sum2(pb[t][2], rs0);
+          rs1 = E::sum2(pb[t][3], rs1);
+        }
+        l_i += rs0 + rs1;
+      }
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        acc[i % DB] = E::mma(va[i % LA_V], pb[i / DB], acc[i % DB]);
+        if (i + LA_V < NPV) va[i % LA_V] = v_operand(buf, (i + LA_V) / DB, (i + LA_V) % DB);
+        // K_{j+1}'s first operands (a harmless stale read after the last tile)
+#pragma unroll
+        for (int r = i * NKP / NPV; r < (i + 1) * NKP / NPV; ++r)
+          kop[r / NB][r % NB] = k_operand(buf ^ 1, r / NB, r % NB);
+      }
+      // MFMA i, then the reads it makes room for (V operands LA_V ahead, K prefetch)
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        const int nreads = (i + LA_V < NPV ? 2 : 0) + ((i + 1) * NKP / NPV - i * NKP / NPV);
+#pragma unroll
+        for (int k = 0; k < nreads; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
-    // keep the K reads LA_S k-steps ahead of the MFMAs that consume them
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
-      if (ks + LA_S < KS) __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
+
+    for (int j = n_active; j < n_tiles_kv; ++j) {
+      const int n0 = kv_begin + j * BN;
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, j & 1);
+      if (j + 1 < n_tiles_kv) issue_v(n0 + BN, (j & 1) ^ 1);
     }
-
     __builtin_amdgcn_s_setprio(0);
-    wait_vmcnt<0>();  // this wave's loads of V_j and K_{j+1} have landed
-    __syncthreads();                // ... every wave's; and every wave is done with K_j
-    if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, buf);
-    if (j + 1 < n_tiles_kv) issue_v(n0 + BN, buf ^ 1);
+  } else {
+    // ---- main loop, software-pipelined across tiles. At head_dim 64 a tile's softmax takes
+    // more issue time than its MFMAs, and two waves per SIMD overlap one's softmax with the
+    // other's MFMAs poorly; each wave therefore interleaves its own. Iteration j runs
+    //   block A  S_{j+1} = K_{j+1} Q^T (MFMA)   interleaved with  softmax_j -> P_j (VALU)
+    //   wait + barrier                           V_j and K_{j+2} have landed; every wave is
+    //                                            done with K_{j+1} and V_{j-1}
+    //   issue K_{j+3} -> K buffer of K_{j+1}, V_{j+1} -> V buffer of V_{j-1}
+    //   block B  O += V_j P_j (MFMA)            interleaved with  the row max of S_{j+1} and
+    //                                            K_{j+2}'s first operand reads
+    //   lazy rescale for tile j+1 (rare), after the PV product it must follow
+    // (C4: +5-7%; at head_dim 128 the same loop is 3% slower, at 32 5% slower). Same two K and
+    // two V buffers; K streams three tiles ahead of its product, V one.
+    constexpr int LA = KS < 2 ? KS : 2;                 // k-steps of K operands read ahead
+    constexpr int NT = BN / 16;                         // 16-key k-steps of O^T
+    constexpr int NPV = NT * DB;                        // MFMAs of the PV product
+    constexpr int LA_V = NPV < 4 ? NPV : 4;             // PV MFMAs whose V operands are read ahead
+    constexpr int KREAD_EVERY = NPV / (LA * NB) > 0 ? NPV / (LA * NB) : 1;
+    constexpr int kVpm = 10, kEpm = 4;                  // VALU / exp instructions per S MFMA
+    u32x4 kop[LA][NB];
+    float m_new = -INFINITY;
 
-    u32x4 va[LA_V];
+    // S^T = K Q^T for the K tile in `buf` (fa2/kernel.py:75-79); kop holds its first LA k-steps
+    auto s_product = [&](f32x16 (&sv)[NB], int buf) {
 #pragma unroll
-    for (int i = 0; i < LA_V; ++i) va[i] = v_operand(buf, i / DB, i % DB);
-
-    // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos. The
-    // condition is uniform over the workgroup (a scalar branch), and one copy of the tile code
-    // serves masked and unmasked tiles so the accumulators keep one register assignment.
-    if (kMaskEveryTile || n0 + BN > full_end) {
+      for (int nb = 0; nb < NB; ++nb) sv[nb] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int slot = ks % LA;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) sv[nb] = E::mma(kop[slot][nb], qreg[ks], sv[nb]);
+        if (ks + LA < KS) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) kop[slot][nb] = k_operand(buf, ks + LA, nb);
+        }
+      }
+    };
+    // masks (fa2/kernel.py:81-88), as in the other loop
+    auto mask_s = [&](f32x16 (&sv)[NB], int n0) {
       const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (nb * 32 + 16 * (i / 8) + (i % 8) > lim) s[nb][i] = -INFINITY;
-    }
-    // online softmax in base 2 (fa2/kernel.py:95-98), with a lazily moved reference max
-    if constexpr (kScaleFirst) {
+          if (nb * 32 + 16 * (i / 8) + (i % 8) > lim) sv[nb][i] = -INFINITY;
+    };
+    // the new reference max (fa2/kernel.py:95), lazily moved; returns whether it moved
+    auto row_max = [&](f32x16 (&sv)[NB]) {
+      if constexpr (kScaleFirst) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) s[nb] *= qk_scale;
-    }
-    float mx = -INFINITY;
+        for (int nb = 0; nb < NB; ++nb) sv[nb] *= qk_scale;
+      }
+      float mx = -INFINITY;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
-    mx = kScaleFirst ? pair_max(mx) : pair_max(mx) * qk_scale;
-    const bool grow = mx > m_i + kRescaleTau;
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-      const float m_new = grow ? mx : m_i;
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[nb][i]);
+      mx = kScaleFirst ? pair_max(mx) : pair_max(mx) * qk_scale;
+      const bool grow = mx > m_i + kRescaleTau;
+      m_new = grow ? mx : m_i;
+      return grow;
+    };
+    // P = exp2(S * scale - m) rounded to the input type, and l (fa2/kernel.py:96-98, 105)
+    auto softmax_p = [&](f32x16 (&sv)[NB], u32x4 (&pb)[NT]) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          sv[nb][i] = __builtin_amdgcn_exp2f(
+              kScaleFirst ? sv[nb][i] - m_i : __builtin_fmaf(sv[nb][i], qk_scale, -m_i));
+      if constexpr (!kRoundedSum) {
+        float rs = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) rs += sv[nb][i];
+        l_i += rs;
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int nb = t >> 1, h = t & 1;
+        pb[t] = u32x4{E::pack2(sv[nb][8 * h + 0], sv[nb][8 * h + 1]),
+                      E::pack2(sv[nb][8 * h + 2], sv[nb][8 * h + 3]),
+                      E::pack2(sv[nb][8 * h + 4], sv[nb][8 * h + 5]),
+                      E::pack2(sv[nb][8 * h + 6], sv[nb][8 * h + 7])};
+      }
+      if constexpr (kRoundedSum) {
+        float rs0 = 0.f, rs1 = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          rs0 = E::sum2(pb[t][0], rs0);
+          rs1 = E::sum2(pb[t][1], rs1);
+          rs0 = E::sum2(pb[t][2], rs0);
+          rs1 = E::sum2(pb[t][3], rs1);
+        }
+        l_i += rs0 + rs1;
+      }
+    };
+    // the unrounded P's sum, for the log-sum-exp output only (a uniform branch)
+    auto exact_sum = [&](const f32x16 (&sv)[NB]) {
+      if (want_exact) {
+        float rx = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) rx += sv[nb][i];
+        l_exact += rx;
+      }
+    };
+    // O^T += V^T P^T for the V tile in `buf` (fa2/kernel.py:100-105)
+    auto pv_product = [&](const u32x4 (&pb)[NT], int buf, u32x4 (&va)[LA_V]) {
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        acc[i % DB] = E::mma(va[i % LA_V], pb[i / DB], acc[i % DB]);
+        if (i + LA_V < NPV) va[i % LA_V] = v_operand(buf, (i + LA_V) / DB, (i + LA_V) % DB);
+      }
+    };
+    auto rescale = [&]() {
       const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
       l_i *= alpha;
       l_exact *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db) acc[db] *= alpha;
       m_i = m_new;
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        s[nb][i] = __builtin_amdgcn_exp2f(kScaleFirst ? s[nb][i] - m_i
-                                                      : __builtin_fmaf(s[nb][i], qk_scale, -m_i));
-    if constexpr (!kRoundedSum) {
-      float rs = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) rs += s[nb][i];
-      l_i += rs;
-    } else if (want_exact) {
-      float rx = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) rx += s[nb][i];
-      l_exact += rx;
-    }
+    };
 
-    // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
-    u32x4 pb[BN / 16];
+    // iteration j (tile j + 1 exists): s_cur holds S_j on entry, s_nxt receives S_{j+1}
+    auto iteration = [&](f32x16 (&s_cur)[NB], f32x16 (&s_nxt)[NB], int j) {
+      const int bufk = (j + 1) & 1;  // K_{j+1}
+      const int bufv = j & 1;        // V_j (and K_{j+2})
+      const int n1 = kv_begin + (j + 1) * BN;
+
+      // block A: each S MFMA, then kVpm VALU and kEpm exp instructions of the softmax
+      u32x4 pb[NT];
+      s_product(s_nxt, bufk);
+      softmax_p(s_cur, pb);
 #pragma unroll
-    for (int t = 0; t < BN / 16; ++t) {
-      const int nb = t >> 1, h = t & 1;
-      pb[t] = u32x4{E::pack2(s[nb][8 * h + 0], s[nb][8 * h + 1]),
-                    E::pack2(s[nb][8 * h + 2], s[nb][8 * h + 3]),
-                    E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
-                    E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
-    }
-    if constexpr (kRoundedSum) {
-      float rs0 = 0.f, rs1 = 0.f;
+      for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int t = 0; t < BN / 16; ++t) {
-        rs0 = E::sum2(pb[t][0], rs0);
-        rs1 = E::sum2(pb[t][1], rs1);
-        rs0 = E::sum2(pb[t][2], rs0);
-        rs1 = E::sum2(pb[t][3], rs1);
+        for (int m = 0; m < NB; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, kVpm, 0);
+          __builtin_amdgcn_sched_group_barrier(0x400, kEpm, 0);
+        }
+        if (ks + LA < KS) __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
       }
-      l_i += rs0 + rs1;
-    }
-    __builtin_amdgcn_s_setprio(1);
+      // P_j and l must be made here, next to the MFMAs, not sunk past the barrier to their use
 #pragma unroll
-    for (int i = 0; i < NPV; ++i) {
-      acc[i % DB] = E::mma(va[i % LA_V], pb[i / DB], acc[i % DB]);
-      if (i + LA_V < NPV) va[i % LA_V] = v_operand(buf, (i + LA_V) / DB, (i + LA_V) % DB);
-      // K_{j+1}'s first operands (a harmless stale read after the last tile)
-#pragma unroll
-      for (int r = i * NKP / NPV; r < (i + 1) * NKP / NPV; ++r)
-        kop[r / NB][r % NB] = k_operand(buf ^ 1, r / NB, r % NB);
-    }
-    // MFMA i, then the reads it makes room for (V operands LA_V ahead, K prefetch)
-#pragma unroll
-    for (int i = 0; i < NPV; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      const int nreads = (i + LA_V < NPV ? 2 : 0) + ((i + 1) * NKP / NPV - i * NKP / NPV);
-#pragma unroll
-      for (int k = 0; k < nreads; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-  }
+      for (int t = 0; t < NT; ++t) asm volatile("" ::"v"(pb[t]));
+      asm volatile("" ::"v"(l_i));
+      exact_sum(s_cur);
 
-  for (int j = n_active; j < n_tiles_kv; ++j) {
-    const int n0 = kv_begin + j * BN;
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (j + 2 < n_tiles_kv) issue_k(n0 + 2 * BN, j & 1);
-    if (j + 1 < n_tiles_kv) issue_v(n0 + BN, (j & 1) ^ 1);
+      wait_vmcnt<0>();  // V_j and K_{j+2} (this wave's part)
+      __syncthreads();  // every wave's; every wave is done with K_{j+1} and V_{j-1}
+      if (j + 3 < n_tiles_kv) issue_k(kv_begin + (j + 3) * BN, bufk);
+      issue_v(n1, bufv ^ 1);
+      if (kMaskEveryTile || n1 + BN > full_end) mask_s(s_nxt, n1);
+
+      // block B: PV_j with the row max of S_{j+1} and K_{j+2}'s first operands in between
+      u32x4 va[LA_V];
+#pragma unroll
+      for (int i = 0; i < LA_V; ++i) va[i] = v_operand(bufv, i / DB, i % DB);
+      const bool grow = row_max(s_nxt);
+      pv_product(pb, bufv, va);
+#pragma unroll
+      for (int ks = 0; ks < LA; ++ks)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand(bufv, ks, nb);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * LA_V, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i + LA_V < NPV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        if (i % KREAD_EVERY == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
+      if (__builtin_amdgcn_ballot_w64(grow)) rescale();
+    };
+
+    f32x16 s_a[NB], s_b[NB];
+    if (n_tiles_kv > 0) {
+      // prologue: K_0, V_0, K_1 in flight; S_0 and its row max; then K_2 into K_0's buffer
+      issue_k(kv_begin, 0);
+      issue_v(kv_begin, 0);
+      if (n_tiles_kv > 1) issue_k(kv_begin + BN, 1);
+      if constexpr (NI % NW == 0 && 2 * JW < 64) {
+        if (n_tiles_kv > 1) wait_vmcnt<2 * JW>();
+        else wait_vmcnt<JW>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < LA; ++ks)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand_v(0, ks, nb);
+      s_product(s_a, 0);
+      wait_vmcnt<0>();
+      __syncthreads();  // V_0 and K_1 have landed; every wave is done with K_0
+      if (n_tiles_kv > 2) issue_k(kv_begin + 2 * BN, 0);
+      if (kMaskEveryTile || kv_begin + BN > full_end) mask_s(s_a, kv_begin);
+      row_max(s_a);
+      m_i = m_new;  // O and l are still zero
+#pragma unroll
+      for (int ks = 0; ks < LA; ++ks)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) kop[ks][nb] = k_operand_v(1, ks, nb);  // stale if 1 tile
+    }
+    // two iterations per trip, so S_j and S_{j+1} alternate between s_a and s_b without copies
+    int j = 0;
+    for (; j + 2 < n_tiles_kv; j += 2) {
+      iteration(s_a, s_b, j);
+      iteration(s_b, s_a, j + 1);
+    }
+    if (j + 1 < n_tiles_kv) {
+      iteration(s_a, s_b, j);
+      ++j;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s_a[nb] = s_b[nb];
+    }
+    if (n_tiles_kv > 0) {
+      // the last tile (j = n_tiles_kv - 1, in s_a): softmax, then its PV product once V landed
+      const int bufv = j & 1;
+      u32x4 pb[NT];
+      softmax_p(s_a, pb);
+      exact_sum(s_a);
+      wait_vmcnt<0>();
+      __syncthreads();
+      u32x4 va[LA_V];
+#pragma unroll
+      for (int i = 0; i < LA_V; ++i) va[i] = v_operand(bufv, i / DB, i % DB);
+      pv_product(pb, bufv, va);
+    }
   }
-  __builtin_amdgcn_s_setprio(0);
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
   const float l = pair_sum(l_i);

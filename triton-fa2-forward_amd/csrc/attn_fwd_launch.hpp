@@ -16,9 +16,10 @@ template <int DT, int D>
 int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsigned grid,
                     hipStream_t stream);
 
-// gfx950 default K/V tile (sweep.py on the BASELINE.json configs, MI355X): 64 keys at
-// head_dim 128 (C2, C3, C5 best), 128 keys at head_dim 64 (C4: 900 vs 857 TFLOP/s).
-constexpr int default_block_n(int head_dim) { return head_dim == 64 ? 128 : 64; }
+// gfx950 default K/V tile: 64 keys (sweep.py on the BASELINE.json configs, MI355X: best for
+// C2, C3, C5 at head_dim 128, and for C4 at head_dim 64 with the software-pipelined loop that
+// 64-key tiles get there).
+constexpr int default_block_n(int /*head_dim*/) { return 64; }
 
 // Launches attn_fwd_kernel<DT, D, 4, default_block_n(D), causal, variant> (128 rows per
 // program), variant in [0, 3]: the timing variants of the product kernel.
