@@ -264,6 +264,20 @@ def test_c_abi_variant_rejects_unknown_bits():
     assert rc == -1 and "head_dim" in _lib.last_error()
 
 
+CAPI_EXE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "capi", "fa2_capi_check")
+
+
+@pytest.mark.skipif(not os.path.exists(CAPI_EXE), reason="tests/capi/fa2_capi_check is built by csrc/build.py")
+def test_c_host_sees_the_c_abi_errors():
+    """The plain-C host (no Python in its process) gets FA2_EINVAL / FA2_EALIGN and the messages
+    for rejected arguments, and the policy queries answer; no GPU call is made."""
+    import subprocess
+
+    res = subprocess.run([CAPI_EXE, "errors"], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "all ok" in res.stdout
+
+
 def test_ablation_skipping_switches_are_not_built():
     from ablation import SKIPPING, attention_ablate
 

@@ -5,7 +5,8 @@
 Compiles attn_fwd_inst.hip once per (dtype, head_dim) pair plus the split-KV combine pass
 (attn_fwd_combine.hip) and the C-ABI file fa2_fwd.hip,
 in parallel, with hipcc for gfx950 only, and links them into
-triton-fa2-forward_amd/fa2/libfa2_fwd.so next to the Python front end that loads it.
+triton-fa2-forward_amd/fa2/libfa2_fwd.so next to the Python front end that loads it. Then builds
+the plain-C host of the C ABI that the tests run (tests/capi/fa2_capi_check).
 """
 
 import argparse
@@ -21,6 +22,7 @@ ROOT = os.path.dirname(PKG)
 INCLUDE = os.path.join(ROOT, "include")
 OBJ_DIR = os.path.join(PKG, "build", "obj")
 LIB_PATH = os.path.join(PKG, "fa2", "libfa2_fwd.so")
+CAPI_DIR = os.path.join(ROOT, "tests", "capi")
 
 ARCH = "gfx950"
 DTYPES = (0, 1)            # 0 = fp16, 1 = bf16
@@ -74,7 +76,23 @@ def build(jobs=8, verbose=False):
     tmp = LIB_PATH + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB_PATH)
+    build_capi_check(verbose)
     return LIB_PATH
+
+
+def build_capi_check(verbose=False):
+    """The plain-C host of the C ABI that tests/test_gpu_capi.py runs (tests/capi/), linked
+    against the library with a relative rpath so that it runs from any checkout."""
+    src = os.path.join(CAPI_DIR, "fa2_capi_check.c")
+    out = os.path.join(CAPI_DIR, "fa2_capi_check")
+    rocm = os.path.dirname(os.path.dirname(os.path.realpath(hipcc())))
+    _run(["gcc", "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+          "-I", os.path.join(rocm, "include"), "-I", INCLUDE, src, "-o", out + ".tmp",
+          "-L", os.path.dirname(LIB_PATH), "-lfa2_fwd", "-L", os.path.join(rocm, "lib"),
+          "-lamdhip64", "-lm", "-Wl,-rpath,$ORIGIN/../../triton-fa2-forward_amd/fa2",
+          "-Wl,-rpath," + os.path.join(rocm, "lib")], verbose)
+    os.replace(out + ".tmp", out)
+    return out
 
 
 def main():
