@@ -206,7 +206,8 @@ void attn_fwd_kernel(const Params p) {
   // sums the unrounded P for the log-sum-exp output. fp16 rounds P 8x finer, so either sum is
   // accurate there; the rounded one (v_dot2, half the instructions) is faster at head_dim 128
   // (+2.5% on C3's shape) and the fp32 one, as in the reference (fa2/kernel.py:98), at 64 and
-  // below (C4: 3.4% faster).
+  // below (C4: 9% faster; with it the fp16 pipelined loop needs 160 VGPRs, three waves per
+  // SIMD, with the rounded sum 173, two).
   constexpr bool kRoundedSum = DT == 1 || D == 128;
   float m_i = -INFINITY;
   float l_i = 0.f;
