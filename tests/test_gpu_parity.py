@@ -226,3 +226,31 @@ def test_kernel_32_key_tiles_pack_and_lengths(causal):
 def test_baseline_config_256_rows_32_keys(name):
     q, k, v, causal = ref.baseline_inputs(name, device="cuda")
     check_against_oracle(q, k, v, causal, precision=torch.float32, block_m=256, block_n=32)
+
+
+# ------------------------------------------------------------------------------------------
+# head_dim 64: the software-pipelined tile loop (64- and 32-key tiles) has its own prologue,
+# a two-tile unrolled body, an odd-count tail and a last-tile epilogue; cover 1 to 6 tiles
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("block_n", [32, 64])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("N", [1, 63, 64, 65, 128, 129, 192, 193, 320, 383])
+def test_pipelined_loop_tile_counts(dtype, block_n, causal, N):
+    q, k, v = make_qkv(BATCH, 4, 2, N, N, 64, dtype)
+    attention = _attention()
+    out, lse = attention(q, k, v, causal=causal, block_n=block_n, return_lse=True)
+    check_against_oracle(q, k, v, causal, ours=out)
+    want = ref.naive_lse(q.double(), k.double(), None, causal=causal)
+    assert (lse.double() - want).abs().max().item() <= 1e-4
+    # without the log-sum-exp: the same kernel, the same bits
+    assert torch.equal(out, attention(q, k, v, causal=causal, block_n=block_n))
+
+
+@pytest.mark.parametrize("splits", [2, 3])
+@pytest.mark.parametrize("N_kv", [130, 700])
+def test_pipelined_loop_split_kv(splits, N_kv):
+    q, k, v = make_qkv(BATCH, 8, 2, 9, N_kv, 64, torch.float16)
+    out = _attention()(q, k, v, causal=False, num_splits=splits)
+    check_against_oracle(q, k, v, False, ours=out)
