@@ -47,8 +47,9 @@ extern "C" {
  *   pack     1, or the GQA group h_q / h_kv: that many query heads share one program
  *            (fa2/kernel.py:233-238); block_m must then be a multiple of pack.
  *   block_m  rows of (position, head) pairs per program, 1..256 (fa2/kernel.py:135-137).
- *   block_n  keys per K/V tile; 0 takes fa2_default_config's (64). The kernel streams K/V
- *            in tiles of 32, 64 or 128 keys and rounds block_n up to the next of these.
+ *   block_n  keys per K/V tile; 0 takes fa2_default_config's (64; 128 at head_dim 16). The
+ *            kernel streams K/V in tiles of 32, 64 or 128 keys and rounds block_n up to the
+ *            next of these.
  *   qk_scale sm_scale * log2(e) > 0 (fa2/kernel.py:240-244).
  *   stream   a hipStream_t (NULL = the default stream of the current device).
  */

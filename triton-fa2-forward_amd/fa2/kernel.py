@@ -42,8 +42,8 @@ def _default_config(head_dim, on_cuda):
     if head_dim not in (16, 32, 64, 128):
         raise ValueError(f"head_dim must be one of 16, 32, 64, 128, got {head_dim}")
     # sweep.py on MI355X: 64-key tiles (C2, C3, C5 at head_dim 128; C4 at 64, where 64-key tiles
-    # get the software-pipelined loop)
-    return 128, 64, 4, 2
+    # get the software-pipelined loop), 128-key tiles at head_dim 16
+    return 128, (128 if head_dim == 16 else 64), 4, 2
 
 
 def _tile_efficiency(rows, block_m):
