@@ -3,6 +3,7 @@
 
     python bench.py [--steps K] [--warmup W] [--config C3] [--all] [--no-cpu-baseline]
     python bench.py --pack-short     # the reference's few-queries table (K/V read rate)
+    python bench.py --all --sdpa     # also torch's own fused SDPA on the same inputs, for context
 
 Workload: BASELINE.json's target config C3 (bf16 causal GQA, B=1, H_q=32, H_kv=8, N=8192,
 D=128), the shape the reference's own bench defaults to (bench/bench.py:228-235) and the one
@@ -108,6 +109,34 @@ def correctness_gate(out, q, k, v, causal):
         except RuntimeError:
             continue
     return None, "unavailable"
+
+
+def sdpa_rate(q, k, v, causal, flops, steps=30):
+    """torch's own fused SDPA on the same inputs (K/V expanded to MHA beforehand, untimed), timed
+    like the headline: settle, then back-to-back steps between one event pair. Context only."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    group = q.shape[1] // k.shape[1]
+    ke = k.repeat_interleave(group, dim=1).contiguous()
+    ve = v.repeat_interleave(group, dim=1).contiguous()
+    for name in ("FLASH_ATTENTION", "EFFICIENT_ATTENTION"):
+        def fn(name=name):
+            with sdpa_kernel(getattr(SDPBackend, name)):
+                return F.scaled_dot_product_attention(q, ke, ve, is_causal=causal)
+        try:
+            fn()
+            torch.cuda.synchronize()
+        except RuntimeError:
+            continue
+        settle_clocks(fn, min_ms=300.0)
+        total_ms, _ = time_steps(fn, steps, 3)
+        ms = total_ms / steps
+        return {"backend": name.lower(), "ms_per_step": round(ms, 5),
+                "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                "note": "torch.nn.functional.scaled_dot_product_attention, K/V expanded to MHA"}
+    return None
 
 
 def settle_clocks(fn, min_ms=1000.0, max_steps=20000):
@@ -259,7 +288,7 @@ def gpu_env():
     }
 
 
-def run(name, steps, warmup, with_cpu, flush_iters):
+def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
     import torch
 
     from fa2 import _lib
@@ -322,6 +351,8 @@ def run(name, steps, warmup, with_cpu, flush_iters):
         fl = flushed_median(fn, flush_iters)
         fl["tflops"] = round(flops / (fl["median_ms"] * 1e-3) / 1e12, 2)
         res["flushed"] = fl
+    if with_sdpa:
+        res["sdpa_same_box"] = sdpa_rate(q, k, v, causal, flops)
     if with_cpu:
         res["cpu_baseline"] = cpu_baseline(name, q, k, v, causal)
     return res
@@ -394,6 +425,8 @@ def main():
     ap.add_argument("--pack-short", action="store_true",
                     help="instead of C3: the reference's few-queries table, one line per N_q")
     ap.add_argument("--flush-iters", type=int, default=10, help="iterations of the flushed pass (0: skip)")
+    ap.add_argument("--sdpa", action="store_true",
+                    help="also time torch's fused SDPA on the same inputs (sdpa_same_box, context)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -414,7 +447,7 @@ def main():
     names = ["C3", "C2", "C4", "C5"] if args.all else [args.config]
     for i, name in enumerate(names):
         res = run(name, args.steps, args.warmup, with_cpu=(i == 0 and not args.no_cpu_baseline),
-                  flush_iters=args.flush_iters)
+                  flush_iters=args.flush_iters, with_sdpa=args.sdpa)
         print(json.dumps(res), flush=True)
 
 
