@@ -254,3 +254,23 @@ def test_pipelined_loop_split_kv(splits, N_kv):
     q, k, v = make_qkv(BATCH, 8, 2, 9, N_kv, 64, torch.float16)
     out = _attention()(q, k, v, causal=False, num_splits=splits)
     check_against_oracle(q, k, v, False, ours=out)
+
+
+# ------------------------------------------------------------------------------------------
+# long sequences: fp32 accumulation over hundreds of tiles, and split-KV over a long K/V
+# ------------------------------------------------------------------------------------------
+
+def test_long_sequence_causal_32k():
+    """bf16 causal GQA at N = 32768 (512 K/V tiles per late program), fp32 oracle per head."""
+    q, k, v = make_qkv(1, 4, 1, 32768, 32768, 128, torch.bfloat16)
+    check_against_oracle(q, k, v, True, precision=torch.float32)
+
+
+@pytest.mark.parametrize("N_q", [1, 64])
+def test_long_kv_few_queries_128k(N_q):
+    """A 131072-key non-causal K/V: the automatic split-KV path, and its log-sum-exp."""
+    q, k, v = make_qkv(1, 8, 2, N_q, 131072, 128, torch.float16)
+    out, lse = _attention()(q, k, v, causal=False, return_lse=True)
+    check_against_oracle(q, k, v, False, precision=torch.float32, ours=out)
+    want = ref.naive_lse(q.float(), k.float(), None, causal=False)
+    assert (lse - want).abs().max().item() <= 1e-4
