@@ -61,10 +61,22 @@ def last_error():
     return lib().fa2_last_error().decode(errors="replace")
 
 
+_STRIDES = {}
+
+
 def _strides(t):
-    # The stride of a size-1 dimension never enters an address; pass 0 so that only the
-    # strides the kernel actually steps by are checked against the 16-byte rule.
-    return (ctypes.c_int64 * 4)(*(0 if n == 1 else s for n, s in zip(t.shape, t.stride())))
+    """The element strides as the C array the ABI takes. The stride of a size-1 dimension never
+    enters an address; pass 0 so that only the strides the kernel actually steps by are checked
+    against the 16-byte rule. The arrays are cached per (shape, strides): the library only reads
+    them during the call, and building one costs more than the rest of a small call."""
+    key = (t.shape, t.stride())
+    arr = _STRIDES.get(key)
+    if arr is None:
+        if len(_STRIDES) >= 1024:
+            _STRIDES.clear()
+        arr = (ctypes.c_int64 * 4)(*(0 if n == 1 else s for n, s in zip(key[0], key[1])))
+        _STRIDES[key] = arr
+    return arr
 
 
 def attn_fwd(q, k, v, out, causal, pack, block_m, block_n, qk_scale, stream):

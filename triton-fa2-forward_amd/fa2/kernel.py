@@ -60,7 +60,11 @@ def should_pack_gqa(n_q, group, block_m):
 
 
 def _loadable(t):
-    """t itself if the kernel's 16-byte loads can address it, else a dense copy."""
+    """t itself if the kernel's 16-byte loads can address it, else a dense copy. A contiguous
+    tensor qualifies when it is 16-byte aligned: its strides are multiples of head_dim, itself a
+    multiple of 8 (the fast path, checked first: this runs four times per call)."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t
     ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
           and all(n == 1 or s % 8 == 0 for n, s in zip(t.shape[:3], t.stride()[:3])))
     return t if ok else t.clone(memory_format=torch.contiguous_format)
@@ -139,7 +143,8 @@ def attention(q, k, v, causal=True, sm_scale=None, block_m=None, block_n=None,
         return (out, lse) if return_lse else out
     q_, k_, v_ = _loadable(q), _loadable(k), _loadable(v)
     o_ = _loadable(out)
-    with torch.cuda.device(q.device):
+
+    def launch():
         stream = torch.cuda.current_stream(q.device).cuda_stream
         if num_splits == 1 and lse is None:
             _lib.attn_fwd(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, stream)
@@ -148,6 +153,14 @@ def attention(q, k, v, causal=True, sm_scale=None, block_m=None, block_n=None,
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
             _lib.attn_fwd_ex(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, lse, num_splits,
                              ws, stream)
+
+    # the launch must run with q's device current; switch only when it is not (the switch costs
+    # more than the rest of a small call)
+    if q.device.index == torch.cuda.current_device():
+        launch()
+    else:
+        with torch.cuda.device(q.device):
+            launch()
     if o_ is not out:
         out.copy_(o_)
     return (out, lse) if return_lse else out
