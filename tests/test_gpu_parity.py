@@ -274,3 +274,16 @@ def test_long_kv_few_queries_128k(N_q):
     check_against_oracle(q, k, v, False, precision=torch.float32, ours=out)
     want = ref.naive_lse(q.float(), k.float(), None, causal=False)
     assert (lse - want).abs().max().item() <= 1e-4
+
+
+# ------------------------------------------------------------------------------------------
+# causal grids whose second round of programs is dealt in reverse (256 < grid <= 768 programs,
+# (batch, kv head) units not a multiple of the 8 XCDs): every program must still run once
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("H,N,D", [(86, 384, 64), (171, 384, 128), (100, 768, 64), (255, 384, 128),
+                                   (193, 512, 64)])
+def test_causal_grid_second_round_order(H, N, D):
+    """Grids of 258, 513, 600, 765 and 772 programs of 128 rows (the last past the window)."""
+    q, k, v = make_qkv(1, H, H, N, N, D, torch.bfloat16)
+    check_against_oracle(q, k, v, True)
