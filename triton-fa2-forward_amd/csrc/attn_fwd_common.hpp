@@ -127,6 +127,19 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// This lane's sum of a score tile (16 values per 32-key block), in index order. It starts from
+// the first value, not from 0.0f: 0 + x cannot be folded (it turns -0 into +0), so a zero start
+// costs one more add per tile; the sum is the same.
+template <int NB>
+__device__ __forceinline__ float lane_sum(const f32x16 (&s)[NB]) {
+  float r = s[0][0];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int i = (nb == 0 ? 1 : 0); i < 16; ++i) r += s[nb][i];
+  return r;
+}
+
 __device__ __forceinline__ u32x2 lds_read_tr(const char FA2_LDS* p) {
   i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 FA2_LDS*)p);
   return __builtin_bit_cast(u32x2, v);

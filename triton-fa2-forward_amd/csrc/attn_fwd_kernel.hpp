@@ -349,19 +349,9 @@ void attn_fwd_kernel(const Params p) {
           s[nb][i] = __builtin_amdgcn_exp2f(kScaleFirst ? s[nb][i] - m_i
                                                         : __builtin_fmaf(s[nb][i], qk_scale, -m_i));
       if constexpr (!kRoundedSum) {
-        float rs = 0.f;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) rs += s[nb][i];
-        l_i += rs;
+        l_i += lane_sum(s);
       } else if (want_exact) {
-        float rx = 0.f;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) rx += s[nb][i];
-        l_exact += rx;
+        l_exact += lane_sum(s);
       }
 
       // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
@@ -484,12 +474,7 @@ void attn_fwd_kernel(const Params p) {
           sv[nb][i] = __builtin_amdgcn_exp2f(
               kScaleFirst ? sv[nb][i] - m_i : __builtin_fmaf(sv[nb][i], qk_scale, -m_i));
       if constexpr (!kRoundedSum) {
-        float rs = 0.f;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) rs += sv[nb][i];
-        l_i += rs;
+        l_i += lane_sum(sv);
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -514,12 +499,7 @@ void attn_fwd_kernel(const Params p) {
     // the unrounded P's sum, for the log-sum-exp output only (a uniform branch)
     auto exact_sum = [&](const f32x16 (&sv)[NB]) {
       if (want_exact) {
-        float rx = 0.f;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) rx += sv[nb][i];
-        l_exact += rx;
+        l_exact += lane_sum(sv);
       }
     };
     // O^T += V^T P^T for the V tile in `buf` (fa2/kernel.py:100-105)
