@@ -287,3 +287,11 @@ def test_causal_grid_second_round_order(H, N, D):
     """Grids of 258, 513, 600, 765 and 772 programs of 128 rows (the last past the window)."""
     q, k, v = make_qkv(1, H, H, N, N, D, torch.bfloat16)
     check_against_oracle(q, k, v, True)
+
+
+@pytest.mark.parametrize("B,H,causal", [(1100, 64, False), (1150, 61, True)])
+def test_grid_beyond_65535_programs(B, H, causal):
+    """70400 and 70150 programs of 16 positions (one program per (batch, head)): the 1-D grid
+    and the program decomposition in both orders (units a multiple of 8 XCDs or not)."""
+    q, k, v = make_qkv(B, H, H, 16, 16, 64, torch.float16)
+    check_against_oracle(q, k, v, causal)
