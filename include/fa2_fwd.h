@@ -62,9 +62,9 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
 
 /*
  * fa2_attn_fwd_ex - fa2_attn_fwd with two optional extensions the reference does not have
- * (its README.md:308-315 lists both as missing): the log-sum-exp of every row and split-KV.
- * No counterpart in the reference's launch; fa2_attn_fwd(...) is fa2_attn_fwd_ex(...,
- * NULL, 1, NULL, 0, stream).
+ * (its README.md:308-315 lists both as missing): the log-sum-exp of every row and split-KV,
+ * and with a workspace that can also hold a key-norm table. No counterpart in the reference's
+ * launch; fa2_attn_fwd(...) is fa2_attn_fwd_ex(..., NULL, 1, NULL, 0, stream).
  *
  *   lse        NULL, or device float[batch * h_q * n_q] (4-byte aligned), row
  *              (b * h_q + h) * n_q + i: log sum_n exp(q_i . k_n * sm_scale) over the keys
@@ -73,9 +73,18 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
  *              that many pieces of whole K/V tiles (fewer if the key range is shorter), one
  *              workgroup each, and a second kernel merges the pieces. For grids too small
  *              to fill the GPU: few queries against a long K/V. fa2_num_splits() picks it.
- *   workspace  device memory of fa2_workspace_bytes(batch, h_q, n_q, head_dim, num_splits)
- *              bytes, 256-byte aligned, when num_splits > 1 (else ignored; may be NULL). The
- *              caller owns it; it must stay untouched until the launch has run.
+ *   workspace  device memory, 256-byte aligned, owned by the caller and untouched until the
+ *              launch has run; may be NULL when num_splits == 1. It must hold at least
+ *              fa2_workspace_bytes(batch, h_q, n_q, head_dim, num_splits) bytes (the split-KV
+ *              partials, 0 without split-KV). fa2_workspace_bytes_for() adds room for a
+ *              key-norm table where it pays; whenever the workspace has that room, a first
+ *              kernel writes every key chunk's largest norm and the attention kernel uses it to
+ *              prove, per row, that later scores cannot pass the row's first-tile max by more
+ *              than 2^15 (fp16) or 2^32 (bf16) in exp2 units, and then skips the per-tile row max.
+ *              Only at the default configuration (block_m <= 128 rounds to 4 waves and the
+ *              default block_n); otherwise the room is left unused. Same attention either way
+ *              (the same 2x-SDPA accuracy); the bits of rows that skip can differ from a launch
+ *              without the table.
  */
 int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
                     const int64_t q_stride[4], const int64_t k_stride[4],
@@ -102,8 +111,8 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
  *
  * Every variant computes the same attention: MASK_EVERY_TILE bit for bit, SCALE_FIRST to fp32
  * rounding of the exponent. Runs at the default configuration (block_m 128,
- * fa2_default_config's block_n), without split-KV or log-sum-exp; the other arguments are
- * those of fa2_attn_fwd. The reference's skipping switches (no_exp, no_softmax, kv_l2) make
+ * fa2_default_config's block_n), without split-KV, log-sum-exp or the key-norm table (variant 0
+ * is fa2_attn_fwd's launch); the other arguments are those of fa2_attn_fwd. The reference's skipping switches (no_exp, no_softmax, kv_l2) make
  * wrong outputs by design and have no entry point.
  */
 int fa2_attn_fwd_variant(const void* q, const void* k, const void* v, void* out,
@@ -119,6 +128,17 @@ int fa2_attn_fwd_variant(const void* q, const void* k, const void* v, void* out,
  */
 size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head_dim,
                            int32_t num_splits);
+
+/*
+ * fa2_workspace_bytes_for - the workspace fa2_attn_fwd_ex can use for this launch:
+ * fa2_workspace_bytes(...) plus, where the key-norm pass pays for itself, room for its table
+ * (one float per batch, kv head and 64 keys). It pays when the attention does at least 16384
+ * FLOP per byte of K and at least 2^37 FLOP: the pass reads K once and saves the per-tile row
+ * max (~4% of the kernel on MI355X). No counterpart in the reference. Host policy only.
+ */
+size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                               int32_t n_kv, int32_t head_dim, int32_t causal,
+                               int32_t num_splits);
 
 /*
  * fa2_num_splits - the split count fa2_attn_fwd_ex should use: 1 for causal launches and for

@@ -30,11 +30,25 @@ constexpr int kXcds = 8;
 constexpr int kCus = 256;
 // Lazy-rescale threshold in exp2 units: the reference max lags the true max by at most this.
 constexpr float kRescaleTau = 8.0f;
+// Score bound from key norms: a wave whose rows all satisfy |q| |k|max qk_scale <= m + tau after
+// their first tile never moves its reference max again, so it skips the row max. P <= 2^tau then:
+// 2^15 stays inside fp16's range (65504); bf16 has fp32's exponent range, so 2^32 is safe there
+// and l and O stay far from fp32 overflow (l <= 2^32 per key).
+template <int DT>
+constexpr float kBoundTau = DT == 1 ? 32.0f : 15.0f;
+// qk_scale raised by 2^-10: covers the fp32 rounding of the squared norms and of the MFMA's
+// score sums (at most ~2^-17 relative at head_dim 128) in the bound |q| |k|max qk_scale.
+__host__ __device__ constexpr float qk_scale_bound(float qk_scale) {
+  return qk_scale * (1.0f + 1.0f / 1024.0f);
+}
 // ln 2: a base-2 log-sum-exp times this is the natural one
 constexpr float kLn2 = 0.6931471805599453f;
 // Kernel variant bits (attn_fwd_kernel's VARIANT; FA2_VARIANT_* in the C ABI)
 constexpr int kVariantScaleFirst = 1;
 constexpr int kVariantMaskEveryTile = 2;
+// Not a timing variant: the instance that reads the key-norm table and skips the row max where
+// the table proves it unneeded (launched by the production path when a table was written).
+constexpr int kVariantKeyBound = 4;
 
 // ---------------------------------------------------------------------------------
 // element type traits: the MFMA, the fp32 -> 16-bit pair conversion (RNE) and the fp32 sum of
@@ -58,6 +72,11 @@ struct Elem<0> {  // fp16
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair),
                                   __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
   }
+  // acc + lo^2 + hi^2 of a packed pair, in fp32
+  static __device__ __forceinline__ float sumsq2(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, pair),
+                                  acc, false);
+  }
 };
 
 template <>
@@ -74,6 +93,11 @@ struct Elem<1> {  // bf16
   static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
                                            __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+  }
+  // acc + lo^2 + hi^2 of a packed pair, in fp32
+  static __device__ __forceinline__ float sumsq2(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
+                                           __builtin_bit_cast(bf16x2, pair), acc, false);
   }
 };
 

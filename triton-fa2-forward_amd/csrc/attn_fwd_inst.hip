@@ -34,6 +34,17 @@ int launch_bn(const Params& p, int block_n, bool causal, unsigned grid, hipStrea
 template <int DT, int D>
 int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsigned grid,
                     hipStream_t s) {
+  if (p.key_norm2) {  // the host writes a key-norm table only for the default configuration
+    constexpr int BN = default_block_n(D);
+    if (waves != 4 || block_n != BN) return (int)hipErrorInvalidValue;
+    if (causal)
+      hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, kVariantKeyBound>), dim3(grid),
+                         dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, kVariantKeyBound>), dim3(grid),
+                         dim3(256), 0, s, p);
+    return (int)hipGetLastError();
+  }
   switch (waves) {
     case 1: return launch_bn<DT, D, 1>(p, block_n, causal, grid, s);
     case 2: return launch_bn<DT, D, 2>(p, block_n, causal, grid, s);

@@ -63,6 +63,7 @@ void attn_fwd_kernel(const Params p) {
   using E = Elem<DT>;
   constexpr bool kScaleFirst = (VARIANT & kVariantScaleFirst) != 0;
   constexpr bool kMaskEveryTile = (VARIANT & kVariantMaskEveryTile) != 0;
+  constexpr bool KB = (VARIANT & kVariantKeyBound) != 0;  // key-norm table present
   constexpr int KS = D / 16;               // 16-dim k-steps of S^T = K Q^T
   constexpr int DB = (D + 31) / 32;        // 32-dim row blocks of O^T
   constexpr int NB = BN / 32;              // 32-key row blocks of S^T
@@ -122,6 +123,54 @@ void attn_fwd_kernel(const Params p) {
     }
   }
   const int n_tiles_kv = (kv_end - kv_begin + BN - 1) / BN;
+
+  // ---- score bound from the key-norm table (fa2_attn_fwd_ex with a workspace): a row's scores
+  // obey |q . k| <= |q| max|k| over the keys it sees. A causal row sees keys [0, pos]: the chunks
+  // before the program's first position (common to its rows: at most four per lane here, the
+  // rest folded at once) and its own last one to three; otherwise every row sees the program's
+  // key range. Either way the bound depends on the row alone, so packed and unpacked launches
+  // decide alike. The table reads are issued here and consumed after the prologue's wait for Q,
+  // by bound_from_table(), so their latency hides behind the Q load. The margin in
+  // qk_scale_bound covers the fp32 rounding of the norms and of the MFMA sums. Without the
+  // table (KB false) the bound is +inf and nothing changes.
+  float kt[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of the common chunks
+  float kr[3] = {0.f, 0.f, 0.f};       // the row's own chunks (causal)
+  if (KB) {
+    const float* kn = p.key_norm2 + (int64_t)(pr.b * (p.h_q / p.group) + pr.hkv) * p.key_chunks;
+    const int c_begin = kv_begin / kKeyChunk;
+    const int c_common = CAUSAL ? lo_pos / kKeyChunk : (kv_end + kKeyChunk - 1) / kKeyChunk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = c_begin + lane + 64 * i;
+      if (c < c_common) kt[i] = kn[c];
+    }
+    for (int c = c_begin + 256 + lane; c < c_common; c += 64) kt[0] = fmaxf(kt[0], kn[c]);
+    if (CAUSAL) {  // 128 positions span at most three 64-key chunks
+      const int c_row = min(pos_vis, kv_end - 1) / kKeyChunk;
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+        if (c_common + t <= c_row) kr[t] = kn[c_common + t];
+    }
+  }
+  auto bound_from_table = [&]() {
+    float km = fmaxf(fmaxf(kt[0], kt[1]), fmaxf(kt[2], kt[3]));
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) km = fmaxf(km, __shfl_xor(km, off, 64));
+    km = fmaxf(km, fmaxf(kr[0], fmaxf(kr[1], kr[2])));
+    float qn = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) qn = E::sumsq2(qreg[ks][w], qn);
+    qn = pair_sum(qn);  // the row's other half of the dims sits in lane ^ 32
+    return __builtin_sqrtf(qn * km) * qk_scale_bound(p.qk_scale);
+  };
+  float bound = INFINITY;
+  // Set after a row's first tile: no later score of the row can exceed its reference max by
+  // more than kBoundTau<DT>, so its reference never moves again (a NaN bound or reference fails
+  // the test). skip_max: every row of the wave is so, and the wave skips the row max.
+  bool skip_row = false;
+  bool skip_max = false;
 
   // ---- K/V staging: each wave issues every NW-th 1 KiB load of the tile. Chunk P of a tile
   // (16 bytes, P = 64 * instruction + lane) holds row P / CPR, logical chunk
@@ -266,6 +315,7 @@ void attn_fwd_kernel(const Params p) {
     // tile of a 128-row program, for its first 64 rows). The wave skips their products and
     // softmax, which would add exact zeros, and keeps only its share of the loads and barriers
     // (the loop after this one). Measured +0.2% on C3, +0.5% on C2, +1.9% on C5.
+    if (KB) bound = bound_from_table();
     int n_active = n_tiles_kv;
     if (CAUSAL) {
       const int wave_last = __builtin_amdgcn_readlane(pos_vis, 31);  // rows grow with the lane
@@ -326,21 +376,27 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) s[nb] *= qk_scale;
       }
-      float mx = -INFINITY;
+      if (!KB || !skip_max) {
+        float mx = -INFINITY;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
-      mx = kScaleFirst ? pair_max(mx) : pair_max(mx) * qk_scale;
-      const bool grow = mx > m_i + kRescaleTau;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float m_new = grow ? mx : m_i;
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-        l_i *= alpha;
-        l_exact *= alpha;
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[nb][i]);
+        mx = kScaleFirst ? pair_max(mx) : pair_max(mx) * qk_scale;
+        const bool grow = !skip_row && mx > m_i + kRescaleTau;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+          const float m_new = grow ? mx : m_i;
+          const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+          l_i *= alpha;
+          l_exact *= alpha;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) acc[db] *= alpha;
-        m_i = m_new;
+          for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+          m_i = m_new;
+        }
+        if (KB && j == 0) {
+          skip_row = bound <= m_i + kBoundTau<DT>;
+          skip_max = __builtin_amdgcn_ballot_w64(!skip_row) == 0;
+        }
       }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -461,7 +517,7 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sv[nb][i]);
       mx = kScaleFirst ? pair_max(mx) : pair_max(mx) * qk_scale;
-      const bool grow = mx > m_i + kRescaleTau;
+      const bool grow = !skip_row && mx > m_i + kRescaleTau;
       m_new = grow ? mx : m_i;
       return grow;
     };
@@ -555,7 +611,8 @@ void attn_fwd_kernel(const Params p) {
       u32x4 va[LA_V];
 #pragma unroll
       for (int i = 0; i < LA_V; ++i) va[i] = v_operand(bufv, i / DB, i % DB);
-      const bool grow = row_max(s_nxt);
+      bool grow = false;
+      if (!KB || !skip_max) grow = row_max(s_nxt);
       pv_product(pb, bufv, va);
 #pragma unroll
       for (int ks = 0; ks < LA; ++ks)
@@ -597,6 +654,11 @@ void attn_fwd_kernel(const Params p) {
       if (kMaskEveryTile || kv_begin + BN > full_end) mask_s(s_a, kv_begin);
       row_max(s_a);
       m_i = m_new;  // O and l are still zero
+      if constexpr (KB) {
+        bound = bound_from_table();
+        skip_row = bound <= m_i + kBoundTau<DT>;
+        skip_max = __builtin_amdgcn_ballot_w64(!skip_row) == 0;
+      }
 #pragma unroll
       for (int ks = 0; ks < LA; ++ks)
 #pragma unroll

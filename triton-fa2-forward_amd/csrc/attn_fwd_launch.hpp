@@ -31,6 +31,10 @@ int launch_attn_fwd_variant(const Params& p, int variant, bool causal, unsigned 
 // Launches the split-KV combine pass (attn_fwd_combine.hip).
 int launch_combine(int dtype, int head_dim, const CombineParams& c, hipStream_t stream);
 
+// Launches the key-norm pass (attn_key_norm.hip) on `grid` = batch * h_kv * chunks workgroups.
+int launch_key_norm(int dtype, int head_dim, const KeyNormParams& k, unsigned grid,
+                    hipStream_t stream);
+
 #define FA2_DECLARE_LAUNCH(DT, D)                                                          \
   extern template int launch_attn_fwd<DT, D>(const Params&, int, int, bool, unsigned, \
                                              hipStream_t);                              \

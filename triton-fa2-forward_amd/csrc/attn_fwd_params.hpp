@@ -5,6 +5,10 @@
 
 namespace fa2 {
 
+// Keys per entry of the key-norm table (attn_key_norm.hip): one workgroup of the key-norm pass
+// each (C3: 1024 workgroups), and at most three entries per 128-row causal program's own rows.
+constexpr int kKeyChunk = 64;
+
 // Kernel arguments: the reference's launch arguments (fa2/kernel.py:248-259) with the
 // d strides dropped (they must be 1) and the grid decomposition precomputed.
 struct Params {
@@ -36,6 +40,20 @@ struct Params {
   int64_t part_rows; // B * H_q * N_q
   int32_t splits;
   int32_t split_tiles;
+  // Optional key-norm table (null: off), written by the key-norm pass before the kernel: for
+  // every (batch, kv head) and every kKeyChunk keys, the largest squared norm of a key. With
+  // it a wave can prove after its first tile that no later score exceeds its reference max by
+  // more than kBoundTau (Cauchy-Schwarz) and then skips the per-tile row max.
+  const float* key_norm2;  // [B * H_kv][key_chunks]
+  int32_t key_chunks;      // ceil(n_kv / kKeyChunk)
+};
+
+// Arguments of the key-norm pass (attn_key_norm.hip).
+struct KeyNormParams {
+  const uint16_t* k;
+  int64_t skb, skh, skn;
+  int32_t h_kv, n_kv, chunks;
+  float* out;  // [B * h_kv][chunks]
 };
 
 // Arguments of the split-KV combine pass: rows are the [B, H_q, N_q] rows of the output.

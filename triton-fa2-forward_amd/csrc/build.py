@@ -3,7 +3,7 @@
     python triton-fa2-forward_amd/csrc/build.py [-j 8] [--verbose]
 
 Compiles attn_fwd_inst.hip once per (dtype, head_dim) pair plus the split-KV combine pass
-(attn_fwd_combine.hip) and the C-ABI file fa2_fwd.hip,
+(attn_fwd_combine.hip), the key-norm pass (attn_key_norm.hip) and the C-ABI file fa2_fwd.hip,
 in parallel, with hipcc for gfx950 only, and links them into
 triton-fa2-forward_amd/fa2/libfa2_fwd.so next to the Python front end that loads it. Then builds
 the plain-C host of the C ABI that the tests run (tests/capi/fa2_capi_check).
@@ -67,7 +67,7 @@ def build(jobs=8, verbose=False):
             obj = os.path.join(OBJ_DIR, f"attn_fwd_dt{dt}_d{d}.o")
             units.append([cc, *common_flags(), f"-DFA2_DT={dt}", f"-DFA2_D={d}", "-c",
                           os.path.join(CSRC, "attn_fwd_inst.hip"), "-o", obj])
-    for name in ("attn_fwd_combine", "fa2_fwd"):
+    for name in ("attn_fwd_combine", "attn_key_norm", "fa2_fwd"):
         units.append([cc, *common_flags(), "-c", os.path.join(CSRC, name + ".hip"),
                       "-o", os.path.join(OBJ_DIR, name + ".o")])
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:

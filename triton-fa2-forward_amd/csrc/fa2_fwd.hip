@@ -99,6 +99,24 @@ WorkspaceLayout workspace_layout(size_t rows, int head_dim, int splits) {
   return w;
 }
 
+// The key-norm table (attn_key_norm.hip): one fp32 per (batch, kv head, kKeyChunk keys),
+// placed after the split-KV partials in the workspace.
+size_t key_table_bytes(int64_t batch, int64_t h_kv, int64_t n_kv) {
+  const int64_t chunks = (n_kv + fa2::kKeyChunk - 1) / fa2::kKeyChunk;
+  return (size_t)((batch * h_kv * chunks * (int64_t)sizeof(float) + 255) & ~(int64_t)255);
+}
+
+// Whether the key-norm pass pays for itself: it reads K once (~K bytes at HBM rate, plus a
+// launch) and saves the per-tile row max, ~4% of the attention kernel's time on MI355X (C3,
+// C4). Worth it when the attention does >= 16384 FLOP per byte of K and runs >= ~0.1 ms.
+bool key_table_pays(int64_t batch, int64_t h_q, int64_t h_kv, int64_t n_q, int64_t n_kv,
+                    int64_t head_dim, bool causal) {
+  const double pairs = causal ? (double)n_q * (n_q + 1) / 2 : (double)n_q * n_kv;
+  const double flops = 4.0 * batch * h_q * pairs * head_dim;
+  const double kbytes = 2.0 * batch * h_kv * n_kv * head_dim;
+  return kbytes > 0 && flops >= 16384.0 * kbytes && flops >= 137438953472.0;  // 2^37
+}
+
 int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
                   const int64_t q_stride[4], const int64_t k_stride[4],
                   const int64_t v_stride[4], const int64_t o_stride[4], int32_t batch,
@@ -154,6 +172,17 @@ size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head
   if (num_splits <= 1 || batch <= 0 || h_q <= 0 || n_q <= 0 || dim_index(head_dim) < 0) return 0;
   const size_t rows = (size_t)batch * h_q * n_q;
   return workspace_layout(rows, head_dim, num_splits).total;
+}
+
+size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                               int32_t n_kv, int32_t head_dim, int32_t causal,
+                               int32_t num_splits) {
+  if (batch <= 0 || h_q <= 0 || h_kv <= 0 || n_q <= 0 || n_kv <= 0 || dim_index(head_dim) < 0)
+    return 0;
+  size_t bytes = fa2_workspace_bytes(batch, h_q, n_q, head_dim, num_splits);
+  if (key_table_pays(batch, h_q, h_kv, n_q, n_kv, head_dim, causal != 0))
+    bytes += key_table_bytes(batch, h_kv, n_kv);
+  return bytes;
 }
 
 int32_t fa2_num_splits(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
@@ -306,6 +335,8 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   p.part_rows = (int64_t)batch * h_q * n_q;
   p.splits = 1;
   p.split_tiles = 0;
+  p.key_norm2 = nullptr;
+  p.key_chunks = 0;
 
   // Split-KV: cut the key range into whole tiles; drop splits that would be empty.
   const int64_t kv_tiles = ((int64_t)n_kv + bn - 1) / bn;
@@ -333,6 +364,31 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
     return fail(FA2_EINVAL, "grid of %lld workgroups is too large", (long long)grid);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // Key-norm table: used whenever the workspace has room for it after the split-KV partials
+  // (fa2_workspace_bytes_for asks for it where it pays).
+  const size_t split_bytes =
+      splits > 1 ? workspace_layout((size_t)p.part_rows, head_dim, splits).total : 0;
+  const size_t table_bytes = key_table_bytes(batch, h_kv, n_kv);
+  if (workspace && n_kv > 0 && workspace_bytes >= split_bytes + table_bytes && variant == 0 &&
+      waves == 4 && bn == default_block_n(head_dim)) {
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+      return fail(FA2_EALIGN, "the workspace must be 256-byte aligned");
+    fa2::KeyNormParams kp;
+    kp.k = p.k;
+    kp.skb = p.skb; kp.skh = p.skh; kp.skn = p.skn;
+    kp.h_kv = h_kv;
+    kp.n_kv = n_kv;
+    kp.chunks = (n_kv + fa2::kKeyChunk - 1) / fa2::kKeyChunk;
+    kp.out = reinterpret_cast<float*>(static_cast<char*>(workspace) + split_bytes);
+    const int64_t kgrid = (int64_t)batch * h_kv * kp.chunks;
+    if (kgrid > 0x7fffffffLL)
+      return fail(FA2_EINVAL, "key-norm grid of %lld workgroups is too large", (long long)kgrid);
+    const int ke = fa2::launch_key_norm(dtype, head_dim, kp, (unsigned)kgrid, st);
+    if (ke != hipSuccess)
+      return fail(FA2_ELAUNCH, "key-norm launch failed: %s", hipGetErrorString((hipError_t)ke));
+    p.key_norm2 = kp.out;
+    p.key_chunks = kp.chunks;
+  }
   int e = variant ? launch_variant(dtype, di, p, variant, causal != 0, (unsigned)grid, st)
                   : launch(dtype, di, p, waves, bn, causal != 0, (unsigned)grid, st);
   if (e != hipSuccess)

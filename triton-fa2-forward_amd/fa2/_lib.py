@@ -27,6 +27,8 @@ SIGNATURES = {
                                             _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                             ctypes.c_float, _i32, _vp]),
     "fa2_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
+    "fa2_workspace_bytes_for": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                                  _i32]),
     "fa2_num_splits": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "fa2_default_config": (ctypes.c_int, [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                           ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
@@ -123,6 +125,22 @@ def attn_fwd_variant(q, k, v, out, causal, pack, qk_scale, variant, stream):
 
 def workspace_bytes(B, H_q, N_q, D, num_splits):
     return int(lib().fa2_workspace_bytes(B, H_q, N_q, D, num_splits))
+
+
+_WS_FOR = {}
+
+
+def workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, causal, num_splits):
+    """fa2_workspace_bytes_for, cached per shape (it is host policy, a pure function)."""
+    key = (B, H_q, H_kv, N_q, N_kv, D, bool(causal), num_splits)
+    n = _WS_FOR.get(key)
+    if n is None:
+        if len(_WS_FOR) >= 1024:
+            _WS_FOR.clear()
+        n = int(lib().fa2_workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, int(bool(causal)),
+                                              num_splits))
+        _WS_FOR[key] = n
+    return n
 
 
 def num_splits(B, H_q, H_kv, N_q, N_kv, D, causal, block_m, block_n, num_cus):

@@ -146,10 +146,11 @@ def attention(q, k, v, causal=True, sm_scale=None, block_m=None, block_n=None,
 
     def launch():
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        if num_splits == 1 and lse is None:
+        # split-KV partials and, on long enough problems, the key-norm table
+        ws_bytes = _lib.workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, causal, num_splits)
+        if ws_bytes == 0 and lse is None:
             _lib.attn_fwd(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, stream)
         else:
-            ws_bytes = _lib.workspace_bytes(B, H_q, N_q, D, num_splits)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
             _lib.attn_fwd_ex(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, lse, num_splits,
                              ws, stream)
