@@ -140,3 +140,18 @@ def test_key_bound_with_split_kv_and_lse(splits):
     check_against_oracle(q, k, v, False, ours=out)
     want = ref.naive_lse(q.double(), k.double(), None, causal=False)
     assert (lse.double() - want).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_key_bound_strided_inputs(causal):
+    """[B, N, H, D] storage viewed as [B, H, N, D] (the reference's strided test,
+    tests/test_correctness.py:216-222): the key-norm pass steps by the sequence stride H*D."""
+    q, k, v = make_qkv(2, 8, 2, 500, 500, 64, torch.bfloat16)
+    q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    out, _, ws = run_with_table(q, k, v, causal)
+    check_against_oracle(q, k, v, causal, ours=out)
+    chunks = -(-500 // CHUNK)
+    got = ws[: 2 * 2 * chunks * 4].view(torch.float32).reshape(2, 2, chunks)
+    norms = torch.zeros(2, 2, chunks * CHUNK, device=k.device)
+    norms[..., :500] = k.float().pow(2).sum(-1)
+    torch.testing.assert_close(got, norms.reshape(2, 2, chunks, CHUNK).amax(-1), rtol=1e-5, atol=0)
