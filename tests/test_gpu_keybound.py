@@ -155,3 +155,14 @@ def test_key_bound_strided_inputs(causal):
     norms = torch.zeros(2, 2, chunks * CHUNK, device=k.device)
     norms[..., :500] = k.float().pow(2).sum(-1)
     torch.testing.assert_close(got, norms.reshape(2, 2, chunks, CHUNK).amax(-1), rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_key_bound_long_key_range(dtype):
+    """40000 keys (625 table entries: the kernel folds the entries past the first 256 in its
+    prologue) against 128 queries, non-causal, with and without split-KV."""
+    q, k, v = make_qkv(1, 4, 1, 128, 40000, 64, dtype)
+    out, _, _ = run_with_table(q, k, v, False)
+    check_against_oracle(q, k, v, False, precision=torch.float32, ours=out)
+    out2, _, _ = run_with_table(q, k, v, False, splits=3)
+    check_against_oracle(q, k, v, False, precision=torch.float32, ours=out2)

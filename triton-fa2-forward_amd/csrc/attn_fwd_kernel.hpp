@@ -144,7 +144,11 @@ void attn_fwd_kernel(const Params p) {
       const int c = c_begin + lane + 64 * i;
       if (c < c_common) kt[i] = kn[c];
     }
-    for (int c = c_begin + 256 + lane; c < c_common; c += 64) kt[0] = fmaxf(kt[0], kn[c]);
+    for (int c0 = c_begin + 256 + lane; c0 < c_common; c0 += 256) {  // past 16384 keys
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (c0 + 64 * i < c_common) kt[i] = fmaxf(kt[i], kn[c0 + 64 * i]);
+    }
     if (CAUSAL) {  // 128 positions span at most three 64-key chunks
       const int c_row = min(pos_vis, kv_end - 1) / kKeyChunk;
 #pragma unroll
