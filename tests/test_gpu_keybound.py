@@ -166,3 +166,42 @@ def test_key_bound_long_key_range(dtype):
     check_against_oracle(q, k, v, False, precision=torch.float32, ours=out)
     out2, _, _ = run_with_table(q, k, v, False, splits=3)
     check_against_oracle(q, k, v, False, precision=torch.float32, ours=out2)
+
+
+def _fuzz_cases(n=48, seed=20261202):
+    import random
+    rnd = random.Random(seed)
+    cases = []
+    for i in range(n):
+        h_kv = rnd.choice([1, 2, 3, 4])
+        group = rnd.choice([1, 2, 4, 7, 8])
+        causal = rnd.random() < 0.5
+        n_q = rnd.choice([1, 17, 64, 129, 300, 777])
+        n_kv = n_q if causal else rnd.choice([1, 64, 65, 500, 1500])
+        d = rnd.choice([16, 32, 64, 128])
+        dtype = rnd.choice([torch.float16, torch.bfloat16])
+        pack = group if (group > 1 and 128 % group == 0 and rnd.random() < 0.5) else 1
+        splits = 1 if causal else rnd.choice([1, 1, 2, 4])
+        lse = rnd.random() < 0.4
+        strided = rnd.random() < 0.25
+        scale = rnd.choice([0.25, 1.0, 3.0])  # small, usual and large scores
+        cases.append((i, rnd.choice([1, 2]), h_kv * group, h_kv, n_q, n_kv, d, dtype, causal, pack,
+                      splits, lse, strided, scale))
+    return cases
+
+
+@pytest.mark.parametrize("case", _fuzz_cases(), ids=lambda c: f"case{c[0]}")
+def test_key_bound_fuzz(case):
+    """Seeded random shapes with the key-norm table forced: every combination of GQA group,
+    packing, lengths, head_dim, dtype, split-KV, log-sum-exp, strides and score scale."""
+    i, B, h_q, h_kv, n_q, n_kv, d, dtype, causal, pack, splits, lse, strided, scale = case
+    print(f"\ncase {case}", flush=True)
+    q, k, v = make_qkv(B, h_q, h_kv, n_q, n_kv, d, dtype, seed=100 + i)
+    q = (q.float() * scale).to(dtype)
+    if strided:
+        q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    out, l, _ = run_with_table(q, k, v, causal, pack=pack, splits=splits, lse=lse)
+    check_against_oracle(q, k, v, causal, precision=torch.float32, ours=out)
+    if lse:
+        want = ref.naive_lse(q.float(), k.float(), None, causal=causal)
+        assert (l - want).abs().max().item() <= 1e-4
