@@ -309,7 +309,7 @@ def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
     # kernels per step: the attention kernel, after the key-norm pass where attention() asks for
     # its table (long problems: fa2_workspace_bytes_for)
     H_kv, N_kv = k.shape[1], k.shape[2]
-    key_norm = (_lib.workspace_bytes_for(B, H_q, H_kv, N, N_kv, D, causal, 1)
+    key_norm = (_lib.workspace_bytes_for(B, H_q, H_kv, N, N_kv, D, q.dtype, causal, 1)
                 > _lib.workspace_bytes(B, H_q, N, D, 1))
     kernels = (["fa2::key_norm_kernel"] if key_norm else []) + ["fa2::attn_fwd_kernel"]
 

@@ -248,22 +248,27 @@ def test_workspace_bytes():
 @needs_lib
 def test_workspace_bytes_for_adds_the_key_table_where_it_pays():
     """The key-norm table (one fp32 per batch, kv head and 64 keys, 256-byte rounded) is asked
-    for when the attention does >= 16384 FLOP per byte of K and >= 2^37 FLOP: BASELINE.json's C3
-    and C4 qualify, C2 (4097 FLOP/B) and C5 (2.2e10 FLOP) and the few-queries shapes do not."""
+    for on bf16 at head_dim 128, or 64 without the causal mask, when the attention does >= 16384
+    FLOP per byte of K and >= 2^37 FLOP: C3 qualifies; C2 (4097 FLOP/B), C5 (2.2e10 FLOP), the
+    fp16 C4 and the few-queries shapes do not."""
     lib = _lib.lib()
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     table = lambda B, H_kv, N_kv: up(B * H_kv * -(-N_kv // 64) * 4)  # noqa: E731
     f = lib.fa2_workspace_bytes_for
-    assert f(1, 32, 8, 8192, 8192, 128, 1, 1) == table(1, 8, 8192)          # C3
-    assert f(2, 16, 16, 16384, 16384, 64, 0, 1) == table(2, 16, 16384)      # C4
-    assert f(4, 16, 16, 4096, 4096, 128, 1, 1) == 0                        # C2
-    assert f(3, 28, 4, 1000, 1000, 128, 1, 1) == 0                         # C5
-    assert f(16, 32, 8, 1, 4096, 128, 0, 2) == lib.fa2_workspace_bytes(16, 32, 1, 128, 2)
+    F16, BF16 = 0, 1
+    assert f(1, 32, 8, 8192, 8192, 128, BF16, 1, 1) == table(1, 8, 8192)          # C3
+    assert f(1, 32, 8, 8192, 8192, 128, F16, 1, 1) == 0                           # fp16: no
+    assert f(2, 16, 16, 16384, 16384, 64, F16, 0, 1) == 0                         # C4 (fp16)
+    assert f(2, 16, 16, 16384, 16384, 64, BF16, 0, 1) == table(2, 16, 16384)      # bf16 full D64
+    assert f(1, 32, 8, 8192, 8192, 64, BF16, 1, 1) == 0                           # causal D64: no
+    assert f(4, 16, 16, 4096, 4096, 128, BF16, 1, 1) == 0                         # C2
+    assert f(3, 28, 4, 1000, 1000, 128, BF16, 1, 1) == 0                          # C5
+    assert f(16, 32, 8, 1, 4096, 128, BF16, 0, 2) == lib.fa2_workspace_bytes(16, 32, 1, 128, 2)
     # split-KV partials first, the table after them
-    assert f(1, 64, 8, 2048, 16384, 128, 0, 2) == (lib.fa2_workspace_bytes(1, 64, 2048, 128, 2)
-                                                   + table(1, 8, 16384))
-    assert f(0, 32, 8, 8192, 8192, 128, 1, 1) == 0
-    assert f(1, 32, 8, 8192, 8192, 48, 1, 1) == 0
+    assert f(1, 64, 8, 2048, 16384, 128, BF16, 0, 2) == (lib.fa2_workspace_bytes(1, 64, 2048, 128, 2)
+                                                         + table(1, 8, 16384))
+    assert f(0, 32, 8, 8192, 8192, 128, BF16, 1, 1) == 0
+    assert f(1, 32, 8, 8192, 8192, 48, BF16, 1, 1) == 0
 
 
 # ------------------------------------------------------------------------------------------

@@ -31,7 +31,7 @@ def test_graph_replays_match_eager(case):
         # per byte of K): two kernels and a workspace per call
         from fa2 import _lib
         shape, kw = (1, 8, 2, 8192, 8192, 128, torch.bfloat16), dict(causal=True)
-        assert _lib.workspace_bytes_for(1, 8, 2, 8192, 8192, 128, True, 1) > 0
+        assert _lib.workspace_bytes_for(1, 8, 2, 8192, 8192, 128, torch.bfloat16, True, 1) > 0
     else:
         shape, kw = (2, 8, 2, 4, 3000, 64, torch.float16), dict(causal=False, num_splits=4,
                                                                   return_lse=True)

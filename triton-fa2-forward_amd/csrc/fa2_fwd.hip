@@ -107,10 +107,18 @@ size_t key_table_bytes(int64_t batch, int64_t h_kv, int64_t n_kv) {
 }
 
 // Whether the key-norm pass pays for itself: it reads K once (~K bytes at HBM rate, plus a
-// launch) and saves the per-tile row max, ~4% of the attention kernel's time on MI355X (C3,
-// C4). Worth it when the attention does >= 16384 FLOP per byte of K and runs >= ~0.1 ms.
+// launch) and saves the per-tile row max where the bound holds. Measured on MI355X against the
+// same launch without the table (N(0,1) inputs unless stated):
+//   bf16 D128 causal +1.4% (C3 +1.6-2.2%), bf16 D128 full +0.3%, bf16 D64 full +4.0%,
+//   bf16 D64 causal -0.9%; fp16 D128 causal -1.8%, fp16 D128 full -2.7%, fp16 D64 full -3.0%
+//   (with C4's half-scale inputs +3.9%), fp16 D64 causal -1.3%.
+// fp16's tau (15, the fp16 range of P) is too tight for unit-variance scores, so the bound
+// fails and the pass is pure cost; bf16's (32) holds. Hence: bf16, head_dim 128 or full
+// attention at 64, and only where the attention does >= 16384 FLOP per byte of K and >= 2^37
+// FLOP (the pass's cost against the ~2-4% it can save).
 bool key_table_pays(int64_t batch, int64_t h_q, int64_t h_kv, int64_t n_q, int64_t n_kv,
-                    int64_t head_dim, bool causal) {
+                    int64_t head_dim, int32_t dtype, bool causal) {
+  if (dtype != FA2_DTYPE_BF16 || !(head_dim == 128 || (head_dim == 64 && !causal))) return false;
   const double pairs = causal ? (double)n_q * (n_q + 1) / 2 : (double)n_q * n_kv;
   const double flops = 4.0 * batch * h_q * pairs * head_dim;
   const double kbytes = 2.0 * batch * h_kv * n_kv * head_dim;
@@ -175,12 +183,12 @@ size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head
 }
 
 size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
-                               int32_t n_kv, int32_t head_dim, int32_t causal,
+                               int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,
                                int32_t num_splits) {
   if (batch <= 0 || h_q <= 0 || h_kv <= 0 || n_q <= 0 || n_kv <= 0 || dim_index(head_dim) < 0)
     return 0;
   size_t bytes = fa2_workspace_bytes(batch, h_q, n_q, head_dim, num_splits);
-  if (key_table_pays(batch, h_q, h_kv, n_q, n_kv, head_dim, causal != 0))
+  if (key_table_pays(batch, h_q, h_kv, n_q, n_kv, head_dim, dtype, causal != 0))
     bytes += key_table_bytes(batch, h_kv, n_kv);
   return bytes;
 }

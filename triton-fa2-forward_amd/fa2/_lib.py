@@ -28,7 +28,7 @@ SIGNATURES = {
                                             ctypes.c_float, _i32, _vp]),
     "fa2_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
     "fa2_workspace_bytes_for": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                                                  _i32]),
+                                                  _i32, _i32]),
     "fa2_num_splits": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "fa2_default_config": (ctypes.c_int, [_i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                           ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
@@ -130,15 +130,15 @@ def workspace_bytes(B, H_q, N_q, D, num_splits):
 _WS_FOR = {}
 
 
-def workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, causal, num_splits):
+def workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, dtype, causal, num_splits):
     """fa2_workspace_bytes_for, cached per shape (it is host policy, a pure function)."""
-    key = (B, H_q, H_kv, N_q, N_kv, D, bool(causal), num_splits)
+    key = (B, H_q, H_kv, N_q, N_kv, D, dtype, bool(causal), num_splits)
     n = _WS_FOR.get(key)
     if n is None:
         if len(_WS_FOR) >= 1024:
             _WS_FOR.clear()
-        n = int(lib().fa2_workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, int(bool(causal)),
-                                              num_splits))
+        n = int(lib().fa2_workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, DTYPE_CODE[dtype],
+                                              int(bool(causal)), num_splits))
         _WS_FOR[key] = n
     return n
 

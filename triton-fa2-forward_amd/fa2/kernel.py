@@ -147,7 +147,8 @@ def attention(q, k, v, causal=True, sm_scale=None, block_m=None, block_n=None,
     def launch():
         stream = torch.cuda.current_stream(q.device).cuda_stream
         # split-KV partials and, on long enough problems, the key-norm table
-        ws_bytes = _lib.workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, causal, num_splits)
+        ws_bytes = _lib.workspace_bytes_for(B, H_q, H_kv, N_q, N_kv, D, q.dtype, causal,
+                                            num_splits)
         if ws_bytes == 0 and lse is None:
             _lib.attn_fwd(q_, k_, v_, o_, causal, pack, bm, bn, qk_scale, stream)
         else:
