@@ -168,6 +168,10 @@ def _call(**over):
     (dict(sq=(8192, 2048, 64, 2)), -2, "stride"),
     (dict(sk=(4096, 2048, 60, 1)), -2, "multiples of 8"),
     (dict(q=0), -1, "null"),
+    # grids past 2^31 - 1 workgroups, including sizes whose product overflows int64
+    (dict(batch=1 << 20, h_q=1 << 20, h_kv=1 << 20, n_q=4096, n_kv=4096), -1, "too large"),
+    (dict(batch=2**31 - 1, h_q=2**31 - 1, h_kv=1, n_q=2**31 - 1, n_kv=2**31 - 1, block_m=1),
+     -1, "too large"),
 ])
 def test_c_abi_rejects_bad_arguments(over, code, msg):
     rc, err = _call(**over)

@@ -333,6 +333,10 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   const int64_t rows = (int64_t)n_q * pack;
   const int64_t n_tiles = (rows + block_m - 1) / block_m;
   const int64_t n_bh = (int64_t)batch * (h_q / pack);
+  // checked before any product with it can leave int64 (n_tiles >= 1: n_q > 0 here)
+  if (n_bh > 0x7fffffffLL / n_tiles)
+    return fail(FA2_EINVAL, "grid of %lld x %lld workgroups is too large", (long long)n_tiles,
+                (long long)n_bh);
   p.n_tiles = (int32_t)n_tiles;
   p.n_bh = (int32_t)n_bh;
   p.qk_scale = qk_scale;
