@@ -168,11 +168,11 @@ def test_key_bound_long_key_range(dtype):
     check_against_oracle(q, k, v, False, precision=torch.float32, ours=out2)
 
 
-def _fuzz_cases(n=48, seed=20261202):
+def _fuzz_cases(n=48, seed=20261202, first=0):
     import random
     rnd = random.Random(seed)
     cases = []
-    for i in range(n):
+    for i in range(first, first + n):
         h_kv = rnd.choice([1, 2, 3, 4])
         group = rnd.choice([1, 2, 4, 7, 8])
         causal = rnd.random() < 0.5
@@ -190,7 +190,8 @@ def _fuzz_cases(n=48, seed=20261202):
     return cases
 
 
-@pytest.mark.parametrize("case", _fuzz_cases(), ids=lambda c: f"case{c[0]}")
+@pytest.mark.parametrize("case", _fuzz_cases() + _fuzz_cases(seed=20261212, first=1000),
+                         ids=lambda c: f"case{c[0]}")
 def test_key_bound_fuzz(case):
     """Seeded random shapes with the key-norm table forced: every combination of GQA group,
     packing, lengths, head_dim, dtype, split-KV, log-sum-exp, strides and score scale."""
