@@ -52,6 +52,9 @@ extern "C" {
  *            next of these.
  *   qk_scale sm_scale * log2(e) > 0 (fa2/kernel.py:240-244).
  *   stream   a hipStream_t (NULL = the default stream of the current device).
+ *   Limits (FA2_EINVAL): at most 2^31 - 1 programs, ceil(n_q * pack / block_m) *
+ *            batch * h_q / pack (times the splits of fa2_attn_fwd_ex); k and v sequence
+ *            strides of at most 2^22 elements (K/V tiles are addressed with 32-bit offsets).
  */
 int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
                  const int64_t q_stride[4], const int64_t k_stride[4],
@@ -80,7 +83,8 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
  *              key-norm table where it pays; whenever the workspace has that room, a first
  *              kernel writes every key chunk's largest norm and the attention kernel uses it to
  *              prove, per row, that later scores cannot pass the row's first-tile max by more
- *              than 2^15 (fp16) or 2^32 (bf16) in exp2 units, and then skips the per-tile row max.
+ *              than 15 (fp16) or 32 (bf16) in exp2 units (a weight of at most 2^15 or
+ *              2^32), and then skips the per-tile row max.
  *              Only at the default configuration (block_m <= 128 rounds to 4 waves and the
  *              default block_n); otherwise the room is left unused. Same attention either way
  *              (the same 2x-SDPA accuracy); the bits of rows that skip can differ from a launch
@@ -112,8 +116,9 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
  * Every variant computes the same attention: MASK_EVERY_TILE bit for bit, SCALE_FIRST to fp32
  * rounding of the exponent. Runs at the default configuration (block_m 128,
  * fa2_default_config's block_n), without split-KV, log-sum-exp or the key-norm table (variant 0
- * is fa2_attn_fwd's launch); the other arguments are those of fa2_attn_fwd. The reference's skipping switches (no_exp, no_softmax, kv_l2) make
- * wrong outputs by design and have no entry point.
+ * is fa2_attn_fwd's launch); the other arguments are those of fa2_attn_fwd. The reference's
+ * skipping switches (no_exp, no_softmax, kv_l2) make wrong outputs by design and have no entry
+ * point.
  */
 int fa2_attn_fwd_variant(const void* q, const void* k, const void* v, void* out,
                          const int64_t q_stride[4], const int64_t k_stride[4],
