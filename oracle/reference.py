@@ -16,8 +16,8 @@ algorithm or helper it is named after:
                                                 as naive_attention: the log-sum-exp output,
                                                 an extension the reference lacks (its
                                                 README.md:308), checked per row
-  errors              tests/test_correctness.py:124-126   max-abs and relative-L2 error
-  acceptance          tests/test_correctness.py:111-113, 172-185   ours <= 2 x SDPA + 1e-4
+  errors              tests/test_correctness.py:42-44   max-abs and relative-L2 error
+  acceptance          tests/test_correctness.py:29-31, 90-103   ours <= 2 x SDPA + 1e-4
   attn_flops          bench/bench.py:83-87      4 B H_q pairs D, causal pairs N(N+1)/2
   baseline_inputs     BASELINE.json "configs"   the five seeded input recipes C1..C5
 
@@ -33,7 +33,7 @@ How each is pinned (tests/test_oracle.py; none of these restates the formula und
                       score + log N), and planted mistakes (mask dropped, base 2 instead of e)
                       that must fail.
   blocked_attention   equal to naive_attention to 1e-5 in fp64 over the reference's own sweep
-                      (tests/test_correctness.py:133-148), with planted mistakes (alpha dropped,
+                      (tests/test_correctness.py:51-66), with planted mistakes (alpha dropped,
                       off-by-one causal mask) that must fail the same check.
   attn_flops          hand counts at small sizes and the published C3 figure (5.49823e11).
   baseline_inputs     shapes, dtypes, seeds and the C5 perturbation count, checked directly.
@@ -45,7 +45,7 @@ import torch
 
 LOG2E = 1.4426950408889634
 
-# Absolute slack of the 2x-SDPA rule (tests/test_correctness.py:111-113).
+# Absolute slack of the 2x-SDPA rule (tests/test_correctness.py:29-31).
 ATOL_FLOOR = 1e-4
 
 
@@ -170,7 +170,7 @@ def blocked_attention(q, k, v, causal=True, sm_scale=None, block_m=32, block_n=1
 
 
 def errors(out, ref):
-    """(max-abs, relative L2) of out against ref, in fp64 (tests/test_correctness.py:124-126)."""
+    """(max-abs, relative L2) of out against ref, in fp64 (tests/test_correctness.py:42-44)."""
     diff = out.double() - ref.double()
     return diff.abs().max().item(), (diff.norm() / ref.double().norm()).item()
 

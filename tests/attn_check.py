@@ -1,4 +1,4 @@
-"""Acceptance helpers shared by the GPU parity tests (restating tests/test_correctness.py:116-185).
+"""Acceptance helpers shared by the GPU parity tests (restating tests/test_correctness.py:29-44, 90-103).
 
 check_against_oracle runs fa2.kernel.attention, the CPU oracle's naive_attention in a high
 precision (fp64 like the reference's tests, or fp32 as BASELINE.json's north star asks) and
@@ -15,7 +15,7 @@ DEVICE = "cuda"
 
 
 def make_qkv(B, H_q, H_kv, N_q, N_kv, D, dtype, seed=0, device=DEVICE):
-    """q, k, v from one seeded generator on the device, in that order (tests/test_correctness.py:116-121)."""
+    """q, k, v from one seeded generator on the device, in that order (tests/test_correctness.py:34-39)."""
     g = torch.Generator(device=device).manual_seed(seed)
     q = torch.randn(B, H_q, N_q, D, device=device, dtype=dtype, generator=g)
     k = torch.randn(B, H_kv, N_kv, D, device=device, dtype=dtype, generator=g)

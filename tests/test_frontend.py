@@ -33,7 +33,7 @@ def cpu_qkv(B, H_q, H_kv, N_q, N_kv, D, dtype=torch.float16):
 # ------------------------------------------------------------------------------------------
 
 def test_should_pack_gqa_follows_tile_efficiency():
-    """tests/test_correctness.py:271-280, verbatim known answers."""
+    """tests/test_correctness.py:189-198, verbatim known answers."""
     assert should_pack_gqa(1, 4, 128)
     assert should_pack_gqa(64, 4, 128)
     assert not should_pack_gqa(4096, 4, 128)
@@ -170,8 +170,19 @@ def _call(**over):
     (dict(q=0), -1, "null"),
     # grids past 2^31 - 1 workgroups, including sizes whose product overflows int64
     (dict(batch=1 << 20, h_q=1 << 20, h_kv=1 << 20, n_q=4096, n_kv=4096), -1, "too large"),
-    (dict(batch=2**31 - 1, h_q=2**31 - 1, h_kv=1, n_q=2**31 - 1, n_kv=2**31 - 1, block_m=1),
+    (dict(batch=2**31 - 1, h_q=2**31 - 1, h_kv=1, n_q=2**31 - 257, n_kv=2**31 - 257, block_m=1),
      -1, "too large"),
+    # 32-bit positions in the kernel: sequences up to 2^31 - 257, causal or not
+    (dict(n_q=2**31 - 1, n_kv=2**31 - 1, block_m=100), -1, "at most"),
+    (dict(causal=0, n_q=32, n_kv=2**31 - 200), -1, "at most"),
+    # a packed launch whose rows (n_q * pack) pass 2^31 although the grid is small: B 1, H 8/1,
+    # N 2^28 + 1 (q is 64 GiB at head_dim 16, which fits in HBM); the row index would wrap
+    (dict(h_q=8, h_kv=1, pack=8, n_q=2**28 + 1, n_kv=2**28 + 1, head_dim=16,
+          sq=(8 * (2**28 + 1) * 16, (2**28 + 1) * 16, 16, 1), sk=((2**28 + 1) * 16, (2**28 + 1) * 16, 16, 1),
+          sv=((2**28 + 1) * 16, (2**28 + 1) * 16, 16, 1), so=(8 * (2**28 + 1) * 16, (2**28 + 1) * 16, 16, 1)),
+     -1, "32-bit row index"),
+    (dict(h_q=8, h_kv=1, pack=8, n_q=2**28 + 1, n_kv=2**28 + 1, block_m=256),
+     -1, "32-bit row index"),
 ])
 def test_c_abi_rejects_bad_arguments(over, code, msg):
     rc, err = _call(**over)

@@ -1,6 +1,6 @@
 """Seeded random shapes through fa2.kernel.attention, against the oracle.
 
-The parity suite follows the reference's grid (tests/test_correctness.py:160-300) and adds
+The parity suite follows the reference's grid (tests/test_correctness.py:106-218) and adds
 chosen edge cases; this file covers the combinations between them: batch, GQA ratio, lengths
 (N_q != N_kv when not causal), head_dim, dtype, packing, tile overrides, split-KV and the
 log-sum-exp, and strided inputs. The case list is fixed by a seed, printed per case, and each

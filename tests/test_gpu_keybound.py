@@ -145,7 +145,7 @@ def test_key_bound_with_split_kv_and_lse(splits):
 @pytest.mark.parametrize("causal", [True, False])
 def test_key_bound_strided_inputs(causal):
     """[B, N, H, D] storage viewed as [B, H, N, D] (the reference's strided test,
-    tests/test_correctness.py:216-222): the key-norm pass steps by the sequence stride H*D."""
+    tests/test_correctness.py:134-140): the key-norm pass steps by the sequence stride H*D."""
     q, k, v = make_qkv(2, 8, 2, 500, 500, 64, torch.bfloat16)
     q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
     out, _, ws = run_with_table(q, k, v, causal)

@@ -1,9 +1,9 @@
 """GPU parity: fa2.kernel.attention (the gfx950 HIP kernel) against the CPU oracle.
 
-The acceptance rule is the reference's (tests/test_correctness.py:172-185): with the oracle's
+The acceptance rule is the reference's (tests/test_correctness.py:90-103): with the oracle's
 naive_attention as ground truth, our max-abs error must be <= 2x that of torch's own fp16/bf16
 SDPA on the same inputs, plus 1e-4, and our output must be finite. The reference's GPU tier
-(tests/test_correctness.py:160-300) is restated case for case; the five BASELINE.json configs are
+(tests/test_correctness.py:106-218) is restated case for case; the five BASELINE.json configs are
 checked at full size against naive_attention computed in fp32, as the north star asks.
 Size-independent invariants (packed == unpacked bit for bit, run-to-run determinism, causal
 prefix independence, closed forms) cover what a tolerance cannot.

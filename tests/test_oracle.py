@@ -3,7 +3,7 @@
 Every check here is independent of the formula under test: committed brute-force golden
 vectors, torch's own SDPA math kernel in fp64, closed forms, and planted mistakes that the
 checks must catch. The blocked recurrence is checked against the naive one exactly as the
-reference checks its own (tests/test_correctness.py:133-148).
+reference checks its own (tests/test_correctness.py:51-66).
 """
 
 import json
@@ -20,7 +20,7 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "att
 
 
 def make_qkv(B, H_q, H_kv, N_q, N_kv, D, dtype, seed=0):
-    """q, k, v from one seeded generator, in that order (tests/test_correctness.py:116-121)."""
+    """q, k, v from one seeded generator, in that order (tests/test_correctness.py:34-39)."""
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(B, H_q, N_q, D, dtype=dtype, generator=g)
     k = torch.randn(B, H_kv, N_kv, D, dtype=dtype, generator=g)
@@ -129,7 +129,7 @@ def test_golden_and_sdpa_checks_catch_planted_mistakes(kind):
 
 
 # ------------------------------------------------------------------------------------------
-# blocked_attention: the reference's own tier-1 sweep (tests/test_correctness.py:133-148)
+# blocked_attention: the reference's own tier-1 sweep (tests/test_correctness.py:51-66)
 # ------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("causal", [True, False])

@@ -187,12 +187,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // (buffer_load_dwordx4 ... lds, LDS destination in M0). Issued as inline asm on purpose: the
 // compiler's own LDS-DMA intrinsic makes it wait for every DMA in flight before the next LDS
 // read of any buffer (it cannot prove the double buffers apart), which serialises the
-// prefetch. Callers wait with wait_vmcnt<N>() before a barrier instead. M0 is used by nothing
-// else in these kernels.
+// prefetch. Callers wait with wait_vmcnt<N>() before a barrier instead. The LDS address is an
+// operand bound to M0 ("{m0}"): the compiler itself writes M0 before the asm and knows it is
+// read there (M0 is a reserved register, so a clobber of it would not be honoured).
 __device__ __forceinline__ void load_lds16(u32x4 desc, uint32_t voffset, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "v"(voffset), "s"(desc), "s"(lds_base)
+               : "v"(voffset), "s"(desc), "{m0}"(lds_base)
                : "memory");
 }
 

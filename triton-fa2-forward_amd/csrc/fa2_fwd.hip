@@ -32,6 +32,9 @@ using fa2::Params;
 constexpr int kDims[4] = {16, 32, 64, 128};
 // 128 rows x stride x 2 bytes must stay below 2^31.
 constexpr int64_t kMaxRowStride = int64_t(1) << 22;
+// Longest sequence: key and query positions stay 32-bit in the kernel with two 128-key tiles
+// of headroom (INT32_MAX - 256).
+constexpr int32_t kMaxSeq = 0x7fffffff - 256;
 
 // Per (dtype, head_dim) launchers, each compiled in its own translation unit.
 int launch(int dtype, int di, const Params& p, int waves, int block_n, bool causal, unsigned grid,
@@ -286,6 +289,11 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
     return fail(FA2_EINVAL, "num_splits must be in [1, %d], got %d", kMaxSplits, num_splits);
   if (num_splits > 1 && causal)
     return fail(FA2_EINVAL, "split-KV needs causal == 0 (the causal kernel skips tiles instead)");
+  // Key positions are 32-bit in the kernel, and its tile loop forms positions up to two K/V
+  // tiles (256 keys) past the last one it loads.
+  if (n_kv > kMaxSeq || n_q > kMaxSeq)
+    return fail(FA2_EINVAL, "n_q and n_kv must be at most %d (32-bit key positions), got %d and %d",
+                kMaxSeq, n_q, n_kv);
   if (batch == 0 || n_q == 0) return FA2_OK;  // empty output: nothing to launch
   // ---- the 16-byte load/store rule
   if (!q || !k || !v || !out) return fail(FA2_EINVAL, "null tensor pointer");
@@ -337,6 +345,12 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   if (n_bh > 0x7fffffffLL / n_tiles)
     return fail(FA2_EINVAL, "grid of %lld x %lld workgroups is too large", (long long)n_tiles,
                 (long long)n_bh);
+  // The kernel's packed row index tile * block_m + (row inside the program) is 32-bit; its
+  // largest value is (n_tiles - 1) * block_m + 32 * waves - 1 (rows past block_m included).
+  if ((n_tiles - 1) * block_m + 32 * waves > 0x7fffffffLL)
+    return fail(FA2_EINVAL,
+                "n_q * pack = %lld rows of block_m %d exceed the kernel's 32-bit row index",
+                (long long)rows, block_m);
   p.n_tiles = (int32_t)n_tiles;
   p.n_bh = (int32_t)n_bh;
   p.qk_scale = qk_scale;
@@ -370,16 +384,21 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
     p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.part_lse);
     p.part_lse_exact = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.part_lse_exact);
     p.splits = splits;
+    // the combine pass runs one thread per 4 dims of every row
+    if (p.part_rows * (head_dim / 4) / 256 >= 0x7fffffffLL)
+      return fail(FA2_EINVAL, "split-KV merge of %lld rows is too large", (long long)p.part_rows);
   }
   const int64_t grid = n_tiles * n_bh * splits;
   if (grid > 0x7fffffffLL)
     return fail(FA2_EINVAL, "grid of %lld workgroups is too large", (long long)grid);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // Key-norm table: used whenever the workspace has room for it after the split-KV partials
-  // (fa2_workspace_bytes_for asks for it where it pays).
+  // Key-norm table: used whenever the workspace has room for it beyond the split-KV partials of
+  // the REQUESTED split count, fa2_workspace_bytes(..., num_splits), which is where
+  // fa2_workspace_bytes_for puts it where it pays. The partials of a clamped (smaller) split
+  // count fit inside that size, so the room they leave never turns the table on by itself.
   const size_t split_bytes =
-      splits > 1 ? workspace_layout((size_t)p.part_rows, head_dim, splits).total : 0;
+      num_splits > 1 ? workspace_layout((size_t)p.part_rows, head_dim, num_splits).total : 0;
   const size_t table_bytes = key_table_bytes(batch, h_kv, n_kv);
   if (workspace && n_kv > 0 && workspace_bytes >= split_bytes + table_bytes && variant == 0 &&
       waves == 4 && bn == default_block_n(head_dim)) {
