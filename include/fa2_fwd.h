@@ -98,6 +98,36 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
                     int32_t block_m, int32_t block_n, float qk_scale, float* lse,
                     int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the library's own device scratch used by fa2_attn_fwd_noalloc (32 MiB per GPU). */
+#define FA2_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * fa2_attn_fwd_noalloc - fa2_attn_fwd_ex without the workspace arguments: it allocates nothing.
+ * No counterpart in the reference. It is for callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ *
+ * The split-KV partials and, where it pays, the key-norm table live in a device array owned by
+ * the library, FA2_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU until the
+ * process ends. Its address is looked up on the first call on each device, which must be the
+ * current device and the stream's. Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (two streams or two threads at once) race; serialise them. The caller still
+ * passes q, k, v, out and lse.
+ *
+ *   num_splits 1..16 as in fa2_attn_fwd_ex; fa2_workspace_bytes(batch, h_q, n_q, head_dim,
+ *              num_splits) must fit in FA2_NOALLOC_SCRATCH_BYTES, else FA2_EINVAL (no launch).
+ *              The key-norm table is used as fa2_attn_fwd_ex with a workspace of
+ *              fa2_workspace_bytes_for(...) bytes uses it, and left off if it would not fit.
+ * With the same arguments the output is bit for bit that of fa2_attn_fwd_ex given a workspace
+ * of fa2_workspace_bytes_for(...) bytes (when that fits in the scratch).
+ */
+int fa2_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
+                         const int64_t q_stride[4], const int64_t k_stride[4],
+                         const int64_t v_stride[4], const int64_t o_stride[4],
+                         int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                         int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                         int32_t block_m, int32_t block_n, float qk_scale, float* lse,
+                         int32_t num_splits, void* stream);
+
 /* Variant bits of fa2_attn_fwd_variant. */
 #define FA2_VARIANT_SCALE_FIRST 1      /* bench/ablation.py:13-14, "scale_first"     */
 #define FA2_VARIANT_MASK_EVERY_TILE 2  /* bench/ablation.py:15, "mask_every_tile"    */

@@ -338,3 +338,18 @@ def test_split_and_lse_arguments_fail_in_python():
         attention(q, q, q, causal=False, num_splits=0)
     with pytest.raises(ValueError, match="causal"):
         attention(q, q, q, causal=True, num_splits=2)
+
+
+@needs_lib
+def test_c_abi_noalloc_rejects_splits_past_its_scratch():
+    """fa2_attn_fwd_noalloc holds FA2_NOALLOC_SCRATCH_BYTES (32 MiB) per GPU: a split-KV launch
+    whose partials need more is rejected before any device call (fake pointers here)."""
+    arr = lambda s: (ctypes.c_int64 * 4)(*s)  # noqa: E731
+    lib = _lib.lib()
+    sq = arr((32 * 64 * 128, 64 * 128, 128, 1))
+    skv = arr((8 * 4096 * 128, 4096 * 128, 128, 1))
+    # B 16, H 32/8, N_q 64, N_kv 4096, 16 splits: 16 x 32768 rows x 128 dims x 4 B = 256 MiB
+    assert lib.fa2_workspace_bytes(16, 32, 64, 128, 16) > 32 << 20
+    rc = lib.fa2_attn_fwd_noalloc(0x1000, 0x2000, 0x3000, 0x4000, sq, skv, skv, sq, 16, 32, 8, 64,
+                                  4096, 128, 0, 0, 1, 128, 0, 0.18, None, 16, None)
+    assert rc == -1 and "scratch" in _lib.last_error(), (rc, _lib.last_error())

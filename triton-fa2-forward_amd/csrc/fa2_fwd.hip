@@ -8,9 +8,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "attn_fwd_launch.hpp"
 #include "fa2_fwd.h"
@@ -243,6 +245,89 @@ int fa2_attn_fwd_variant(const void* q, const void* k, const void* v, void* out,
   return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
                        n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
                        nullptr, 0, variant, stream);
+}
+
+}  // extern "C"
+
+// ---- the no-allocation entry point: its workspace is this library's own device memory.
+// One copy per GPU, alive until the process ends; every call on a GPU shares it, so calls that
+// overlap on one GPU (two streams, two threads) race. Nothing in it needs clearing between
+// calls: the split-KV partials and the key-norm table are written in full before they are read.
+static __device__ __align__(256) unsigned char scratch[FA2_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of `scratch` on the GPU that `stream` runs on, which must be the current one.
+// Looked up once per device (hipGetSymbolAddress with that device current) and kept: the array's
+// host-side name is only a stand-in and must never reach a kernel.
+int scratch_on_stream_device(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FA2_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess)
+      return fail(FA2_ELAUNCH, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(FA2_EINVAL,
+                  "the stream runs on device %d but device %d is current; make it current", sdev,
+                  dev);
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(FA2_EINVAL, "device %d is past the %d devices the scratch table covers", dev,
+                kMaxScratchDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(FA2_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FA2_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa2_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
+                         const int64_t q_stride[4], const int64_t k_stride[4],
+                         const int64_t v_stride[4], const int64_t o_stride[4],
+                         int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                         int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                         int32_t block_m, int32_t block_n, float qk_scale, float* lse,
+                         int32_t num_splits, void* stream) {
+  g_err[0] = '\0';
+  // the split-KV partials are required; the key-norm table (where it pays) is optional and is
+  // left off when it would not fit beside them
+  const size_t need = fa2_workspace_bytes(batch, h_q, n_q, head_dim, num_splits);
+  if (need > (size_t)FA2_NOALLOC_SCRATCH_BYTES)
+    return fail(FA2_EINVAL,
+                "split-KV with %d splits needs %zu bytes of scratch; fa2_attn_fwd_noalloc holds "
+                "%zu (use fa2_attn_fwd_ex with a workspace, or fewer splits)",
+                num_splits, need, (size_t)FA2_NOALLOC_SCRATCH_BYTES);
+  size_t use = fa2_workspace_bytes_for(batch, h_q, h_kv, n_q, n_kv, head_dim, dtype, causal,
+                                       num_splits);
+  if (use > (size_t)FA2_NOALLOC_SCRATCH_BYTES) use = need;
+  void* ws = nullptr;
+  if (use > 0) {
+    const int rc = scratch_on_stream_device(stream, &ws);
+    if (rc != FA2_OK) return rc;
+  }
+  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                       n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale, lse,
+                       num_splits, ws, use, 0, stream);
 }
 
 }  // extern "C"

@@ -23,6 +23,9 @@ SIGNATURES = {
                                        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _i32, _i32, ctypes.c_float, _vp, _i32, _vp,
                                        ctypes.c_size_t, _vp]),
+    "fa2_attn_fwd_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
+                                            _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                            _i32, _i32, ctypes.c_float, _vp, _i32, _vp]),
     "fa2_attn_fwd_variant": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
                                             _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                             ctypes.c_float, _i32, _vp]),
@@ -108,6 +111,21 @@ def attn_fwd_ex(q, k, v, out, causal, pack, block_m, block_n, qk_scale, lse, num
         0 if workspace is None else workspace.numel(), stream)
     if rc != 0:
         raise RuntimeError(f"fa2_attn_fwd_ex failed ({rc}): {last_error()}")
+
+
+def attn_fwd_noalloc(q, k, v, out, causal, pack, block_m, block_n, qk_scale, lse, num_splits,
+                     stream):
+    """Call fa2_attn_fwd_noalloc: fa2_attn_fwd_ex with the library's own scratch as the
+    workspace (no allocation anywhere); lse (fp32 [B, H_q, N_q]) may be None."""
+    B, H_q, N_q, D = q.shape
+    H_kv, N_kv = k.shape[1], k.shape[2]
+    rc = lib().fa2_attn_fwd_noalloc(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+        _strides(q), _strides(k), _strides(v), _strides(out),
+        B, H_q, H_kv, N_q, N_kv, D, DTYPE_CODE[q.dtype], int(bool(causal)), pack,
+        block_m, block_n, qk_scale, None if lse is None else lse.data_ptr(), num_splits, stream)
+    if rc != 0:
+        raise RuntimeError(f"fa2_attn_fwd_noalloc failed ({rc}): {last_error()}")
 
 
 def attn_fwd_variant(q, k, v, out, causal, pack, qk_scale, variant, stream):
