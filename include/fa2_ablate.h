@@ -1,0 +1,69 @@
+/*
+ * fa2_ablate.h - C ABI of libfa2_ablate.so, the measurement library of the gfx950
+ * FlashAttention-2 forward. It is not part of the drop-in: fa2.kernel never loads it, and
+ * libfa2_fwd.so exports none of this.
+ *
+ * The reference attributes its kernel's time with a knockout copy of the kernel whose switches
+ * each change or remove one kind of work (bench/ablation.py:1-20, the copy at 56-202,
+ * `attention_ablate` at 182-200). Here every variant is the product's kernel template
+ * (attn_fwd_kernel) instantiated with VARIANT bits, so a variant differs from the product in the
+ * switched work only. Variants that skip work compute wrong outputs on purpose: only their time
+ * means anything.
+ *
+ * Return convention as in fa2_fwd.h: 0 on success, FA2_EINVAL / FA2_EALIGN / FA2_ELAUNCH on a
+ * rejected argument or a failed launch, with fa2_ablate_last_error() describing it.
+ */
+#ifndef FA2_ABLATE_H
+#define FA2_ABLATE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "fa2_fwd.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Switch bits (bench/ablation.py:6-17). */
+#define FA2_ABLATE_SCALE_FIRST 1       /* scale every score, then subtract the row max: two VALU
+                                          instructions per score instead of one FMA (:13-14)   */
+#define FA2_ABLATE_MASK_EVERY_TILE 2   /* mask every K/V tile, not only those that need it (:15) */
+#define FA2_ABLATE_NO_EXP 8            /* exp2 replaced by its argument, alpha too (:6)         */
+#define FA2_ABLATE_NO_SOFTMAX 16       /* no mask, max, exp, sum or rescale: O = (Q K^T) V (:7)  */
+#define FA2_ABLATE_KV_L2 32            /* every K/V tile load reads the first tile again, so it
+                                          hits L2 instead of HBM (:8-9)                          */
+
+/*
+ * fa2_ablate_attn_fwd - the forward kernel with the switches in `variant`.
+ *
+ *   variant  one of the reference's variants (bench/ablation.py:42-53):
+ *              0                                          copy (the product kernel, bit for bit
+ *                                                         equal to fa2_attn_fwd's launch)
+ *              FA2_ABLATE_SCALE_FIRST                     scale_first
+ *              FA2_ABLATE_MASK_EVERY_TILE                 mask_every_tile
+ *              FA2_ABLATE_SCALE_FIRST | ..._MASK_EVERY_TILE   before_fixes
+ *              FA2_ABLATE_NO_EXP                          no_exp
+ *              FA2_ABLATE_NO_SOFTMAX                      no_softmax
+ *              FA2_ABLATE_KV_L2                           kv_l2
+ *              FA2_ABLATE_NO_SOFTMAX | FA2_ABLATE_KV_L2   matmul_only
+ *            other bit sets are rejected (FA2_EINVAL).
+ * The other arguments are fa2_attn_fwd's (include/fa2_fwd.h), with the same checks. Runs at the
+ * default configuration (block_m 128, fa2_default_config's block_n), without split-KV, the
+ * log-sum-exp or the key-norm table: variant 0 is exactly fa2_attn_fwd's kernel.
+ */
+FA2_API int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                                const int64_t q_stride[4], const int64_t k_stride[4],
+                                const int64_t v_stride[4], const int64_t o_stride[4],
+                                int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                                int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,
+                                int32_t pack, float qk_scale, int32_t variant, void* stream);
+
+/* Thread-local description of this library's last failure in this thread ("" if none). */
+FA2_API const char* fa2_ablate_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA2_ABLATE_H */

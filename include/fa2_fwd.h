@@ -26,6 +26,13 @@ extern "C" {
 #define FA2_DTYPE_F16 0
 #define FA2_DTYPE_BF16 1
 
+/* Every entry point is exported from the shared library; everything else in it is hidden. */
+#if defined(__GNUC__)
+#define FA2_API __attribute__((visibility("default")))
+#else
+#define FA2_API
+#endif
+
 #define FA2_OK 0
 #define FA2_EINVAL (-1)      /* an argument violates the contract below */
 #define FA2_EALIGN (-2)      /* a pointer or stride breaks the 16-byte load rule */
@@ -56,12 +63,12 @@ extern "C" {
  *            batch * h_q / pack (times the splits of fa2_attn_fwd_ex); k and v sequence
  *            strides of at most 2^22 elements (K/V tiles are addressed with 32-bit offsets).
  */
-int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
-                 const int64_t q_stride[4], const int64_t k_stride[4],
-                 const int64_t v_stride[4], const int64_t o_stride[4],
-                 int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
-                 int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
-                 int32_t block_m, int32_t block_n, float qk_scale, void* stream);
+FA2_API int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                         const int64_t q_stride[4], const int64_t k_stride[4],
+                         const int64_t v_stride[4], const int64_t o_stride[4],
+                         int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                         int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                         int32_t block_m, int32_t block_n, float qk_scale, void* stream);
 
 /*
  * fa2_attn_fwd_ex - fa2_attn_fwd with two optional extensions the reference does not have
@@ -90,13 +97,13 @@ int fa2_attn_fwd(const void* q, const void* k, const void* v, void* out,
  *              (the same 2x-SDPA accuracy); the bits of rows that skip can differ from a launch
  *              without the table.
  */
-int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
-                    const int64_t q_stride[4], const int64_t k_stride[4],
-                    const int64_t v_stride[4], const int64_t o_stride[4],
-                    int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
-                    int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
-                    int32_t block_m, int32_t block_n, float qk_scale, float* lse,
-                    int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
+FA2_API int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
+                            const int64_t q_stride[4], const int64_t k_stride[4],
+                            const int64_t v_stride[4], const int64_t o_stride[4],
+                            int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                            int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                            int32_t block_m, int32_t block_n, float qk_scale, float* lse,
+                            int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Size of the library's own device scratch used by fa2_attn_fwd_noalloc (32 MiB per GPU). */
 #define FA2_NOALLOC_SCRATCH_BYTES (32u << 20)
@@ -120,49 +127,20 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
  * With the same arguments the output is bit for bit that of fa2_attn_fwd_ex given a workspace
  * of fa2_workspace_bytes_for(...) bytes (when that fits in the scratch).
  */
-int fa2_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
-                         const int64_t q_stride[4], const int64_t k_stride[4],
-                         const int64_t v_stride[4], const int64_t o_stride[4],
-                         int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
-                         int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
-                         int32_t block_m, int32_t block_n, float qk_scale, float* lse,
-                         int32_t num_splits, void* stream);
-
-/* Variant bits of fa2_attn_fwd_variant. */
-#define FA2_VARIANT_SCALE_FIRST 1      /* bench/ablation.py:13-14, "scale_first"     */
-#define FA2_VARIANT_MASK_EVERY_TILE 2  /* bench/ablation.py:15, "mask_every_tile"    */
-
-/*
- * fa2_attn_fwd_variant - the forward kernel with the reference's two non-skipping ablation
- * switches, for timing the design choices they undo. Counterpart of `attention_ablate`'s
- * scale_first / mask_every_tile (bench/ablation.py:11-17, 182-200), which launch a copy of
- * `_attn_fwd`; here the switches are compile-time flags of the one kernel template.
- *
- *   variant  0, or an OR of FA2_VARIANT_SCALE_FIRST (multiply every score by the scale, then
- *            subtract the row max: two instructions per score instead of one FMA) and
- *            FA2_VARIANT_MASK_EVERY_TILE (apply the causal / end-of-sequence mask on every K/V
- *            tile, not only on the tiles that need it). 0 runs the production kernel.
- *
- * Every variant computes the same attention: MASK_EVERY_TILE bit for bit, SCALE_FIRST to fp32
- * rounding of the exponent. Runs at the default configuration (block_m 128,
- * fa2_default_config's block_n), without split-KV, log-sum-exp or the key-norm table (variant 0
- * is fa2_attn_fwd's launch); the other arguments are those of fa2_attn_fwd. The reference's
- * skipping switches (no_exp, no_softmax, kv_l2) make wrong outputs by design and have no entry
- * point.
- */
-int fa2_attn_fwd_variant(const void* q, const void* k, const void* v, void* out,
-                         const int64_t q_stride[4], const int64_t k_stride[4],
-                         const int64_t v_stride[4], const int64_t o_stride[4],
-                         int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
-                         int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
-                         float qk_scale, int32_t variant, void* stream);
+FA2_API int fa2_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
+                                 const int64_t q_stride[4], const int64_t k_stride[4],
+                                 const int64_t v_stride[4], const int64_t o_stride[4],
+                                 int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                                 int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
+                                 int32_t block_m, int32_t block_n, float qk_scale, float* lse,
+                                 int32_t num_splits, void* stream);
 
 /*
  * fa2_workspace_bytes - workspace size of a split-KV launch of fa2_attn_fwd_ex: fp32 partial
  * outputs and log-sum-exps of every split. 0 when num_splits <= 1 or a size is not positive.
  */
-size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head_dim,
-                           int32_t num_splits);
+FA2_API size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head_dim,
+                                   int32_t num_splits);
 
 /*
  * fa2_workspace_bytes_for - the workspace fa2_attn_fwd_ex can use for this launch:
@@ -174,9 +152,9 @@ size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int32_t head
  * fails on unit-variance scores, and the pass then costs 1-3%. No counterpart in the
  * reference. Host policy only.
  */
-size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
-                               int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,
-                               int32_t num_splits);
+FA2_API size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                                       int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,
+                                       int32_t num_splits);
 
 /*
  * fa2_num_splits - the split count fa2_attn_fwd_ex should use: 1 for causal launches and for
@@ -185,9 +163,9 @@ size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t
  * smaller of the packed and the unpacked GQA layouts, so the answer does not depend on the
  * packing decision and packed and unpacked launches stay equal bit for bit. Host policy only.
  */
-int32_t fa2_num_splits(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
-                       int32_t head_dim, int32_t causal, int32_t block_m, int32_t block_n,
-                       int32_t num_cus);
+FA2_API int32_t fa2_num_splits(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv,
+                               int32_t head_dim, int32_t causal, int32_t block_m, int32_t block_n,
+                               int32_t num_cus);
 
 /*
  * fa2_default_config - the gfx950 tile configuration for a head dim.
@@ -196,21 +174,21 @@ int32_t fa2_num_splits(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, in
  * workgroup, the counterpart of Triton's num_warps) and num_stages (K/V buffers in
  * flight). Returns FA2_EINVAL for an unsupported head_dim.
  */
-int fa2_default_config(int32_t head_dim, int32_t* block_m, int32_t* block_n,
-                       int32_t* num_waves, int32_t* num_stages);
+FA2_API int fa2_default_config(int32_t head_dim, int32_t* block_m, int32_t* block_n,
+                               int32_t* num_waves, int32_t* num_stages);
 
 /*
  * fa2_should_pack_gqa - FlashAttention-3's packing rule, as `should_pack_gqa`
  * (fa2/kernel.py:198-207): 1 when group > 1, block_m % group == 0 and the unpacked
  * tiles are less than 90% as full as the packed ones; else 0.
  */
-int fa2_should_pack_gqa(int32_t n_q, int32_t group, int32_t block_m);
+FA2_API int fa2_should_pack_gqa(int32_t n_q, int32_t group, int32_t block_m);
 
 /* Thread-local description of the last failure in this thread ("" if none). */
-const char* fa2_last_error(void);
+FA2_API const char* fa2_last_error(void);
 
 /* Library version string, including the gfx target it was built for. */
-const char* fa2_version(void);
+FA2_API const char* fa2_version(void);
 
 #ifdef __cplusplus
 }

@@ -287,22 +287,89 @@ def test_workspace_bytes_for_adds_the_key_table_where_it_pays():
 
 
 # ------------------------------------------------------------------------------------------
-# fa2_attn_fwd_variant / attention_ablate: the timing variants (reference bench/ablation.py)
+# the measurement library libfa2_ablate.so (include/fa2_ablate.h): the timing variants of the
+# reference's bench/ablation.py, kept out of the product library
 # ------------------------------------------------------------------------------------------
 
+ABLATE_HEADER = os.path.join(ROOT, "include", "fa2_ablate.h")
+ABLATE_LIB = os.path.join(ROOT, "triton-fa2-forward_amd", "libfa2_ablate.so")
+needs_ablate = pytest.mark.skipif(not os.path.exists(ABLATE_LIB), reason="libfa2_ablate.so not built")
+
+
+def _exported(path):
+    """Names of the functions a shared library exports (nm -D --defined-only)."""
+    import shutil
+    import subprocess
+
+    if not shutil.which("nm"):
+        pytest.skip("nm (binutils) is not installed")
+    res = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True)
+    return {line.split()[-1] for line in res.stdout.splitlines() if line.strip()}
+
+
+def _c_names(header):
+    text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+    return set(re.findall(r"\b(fa2_[a-z0-9_]+)\s*\(", text))
+
+
 @needs_lib
-def test_c_abi_variant_rejects_unknown_bits():
+def test_product_library_exports_its_api_and_no_timing_variant():
+    """libfa2_fwd.so exports exactly the C functions of fa2_fwd.h (hidden visibility for the
+    rest), and none of the measurement library's: no ablation entry point, and no kernel
+    instance with a timing-variant bit (only VARIANT 0, the product, and 4, its key-norm
+    instance, are compiled in)."""
+    names = _exported(_lib.LIB_PATH)
+    c_funcs = {n for n in names if n.startswith("fa2_")}
+    assert c_funcs == _declared_functions()
+    assert not {n for n in names if "ablate" in n or "variant" in n}
+    kernels = [n for n in names if n.startswith("_ZN3fa215attn_fwd_kernel")]
+    assert kernels
+    for n in kernels:
+        variant = int(re.search(r"ELb[01]ELi(\d+)EEEv", n).group(1))
+        assert variant in (0, 4), n
+
+
+@needs_ablate
+def test_measurement_library_exports_exactly_its_header():
+    names = _exported(ABLATE_LIB)
+    assert {n for n in names if n.startswith("fa2_")} == _c_names(ABLATE_HEADER) == {
+        "fa2_ablate_attn_fwd", "fa2_ablate_last_error"}
+    # the knockouts are compiled into it: kernel instances with the no_exp, no_softmax and
+    # kv_l2 bits, and matmul_only (no_softmax | kv_l2)
+    variants = {int(m.group(1)) for n in names for m in [re.search(r"ELb[01]ELi(\d+)EEEv", n)] if m}
+    assert variants == {0, 1, 2, 3, 8, 16, 32, 48}
+
+
+@needs_ablate
+def test_measurement_library_rejects_unbuilt_variants_before_any_launch():
+    from ablation import ablate_lib
+
     arr = lambda s: (ctypes.c_int64 * 4)(*s)  # noqa: E731
-    lib = _lib.lib()
+    lib = ablate_lib()
     st = arr((8192, 2048, 64, 1))
-    for bad in (4, 8, -1):
-        rc = lib.fa2_attn_fwd_variant(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
-                                      32, 64, 0, 1, 1, 0.18, bad, None)
-        assert rc == -1 and "variant" in _lib.last_error(), (bad, rc)
-    # the shared argument checks apply to every variant
-    rc = lib.fa2_attn_fwd_variant(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
-                                  32, 48, 0, 1, 1, 0.18, 1, None)
-    assert rc == -1 and "head_dim" in _lib.last_error()
+    for bad in (4, 5, 24, 64, -1):      # 4: the key-norm instance is the product's, not a variant
+        rc = lib.fa2_ablate_attn_fwd(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
+                                     32, 64, 0, 1, 1, 0.18, bad, None)
+        assert rc == -1 and b"variant" in lib.fa2_ablate_last_error(), (bad, rc)
+    # the product's argument checks apply to every variant
+    rc = lib.fa2_ablate_attn_fwd(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
+                                 32, 48, 0, 1, 1, 0.18, 8, None)
+    assert rc == -1 and b"head_dim" in lib.fa2_ablate_last_error()
+
+
+def test_ablation_front_end_checks_arguments_on_the_cpu():
+    from ablation import VARIANTS, attention_ablate, variant_bits
+
+    # the reference's variant names (bench/ablation.py:42-53) and their bits
+    assert list(VARIANTS) == ["copy", "scale_first", "mask_every_tile", "before_fixes", "no_exp",
+                              "no_softmax", "kv_l2", "matmul_only", "pack"]
+    assert variant_bits(VARIANTS["matmul_only"]) == 48
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
+    with pytest.raises(AssertionError, match="unknown"):
+        attention_ablate(q, q, q, fast=True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        attention_ablate(q, q, q, no_exp=True)
 
 
 CAPI_EXE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "capi", "fa2_capi_check")
@@ -317,19 +384,6 @@ def test_c_host_sees_the_c_abi_errors():
     res = subprocess.run([CAPI_EXE, "errors"], capture_output=True, text=True, timeout=60)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "all ok" in res.stdout
-
-
-def test_ablation_skipping_switches_are_not_built():
-    from ablation import SKIPPING, attention_ablate
-
-    q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
-    for knob in SKIPPING:
-        with pytest.raises(ValueError, match="skip work"):
-            attention_ablate(q, q, q, **{knob: True})
-    with pytest.raises(AssertionError, match="unknown"):
-        attention_ablate(q, q, q, fast=True)
-    with pytest.raises(RuntimeError, match="GPU"):
-        attention_ablate(q, q, q, scale_first=True)
 
 
 def test_split_and_lse_arguments_fail_in_python():
@@ -353,3 +407,22 @@ def test_c_abi_noalloc_rejects_splits_past_its_scratch():
     rc = lib.fa2_attn_fwd_noalloc(0x1000, 0x2000, 0x3000, 0x4000, sq, skv, skv, sq, 16, 32, 8, 64,
                                   4096, 128, 0, 0, 1, 128, 0, 0.18, None, 16, None)
     assert rc == -1 and "scratch" in _lib.last_error(), (rc, _lib.last_error())
+
+
+@needs_lib
+def test_build_records_the_resources_of_every_product_instance():
+    """csrc/build.py keeps the compiler's resource report of every attn_fwd_kernel instance
+    (fa2/kernel_resources.json), and sweep.py finds the instance any tile choice runs."""
+    import sweep
+
+    res = sweep.load_resources()
+    assert res, "kernel_resources.json missing or empty"
+    for dt in (0, 1):
+        for d in (16, 32, 64, 128):
+            for causal in (False, True):
+                for bm in (1, 32, 64, 100, 128, 256):
+                    for bn in (16, 32, 64, 128):
+                        r = res[sweep.instance_name(dt, d, bm, bn, causal, False)]
+                        assert r["vgprs"] > 0 and r["lds_bytes"] > 0 and r["waves_per_simd"] >= 1
+                r = res[sweep.instance_name(dt, d, 128, 0 or _default_config(d, True)[1], causal, True)]
+                assert r["variant"] == 4

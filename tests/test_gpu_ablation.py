@@ -1,13 +1,15 @@
-"""The kernel's timing variants (triton-fa2-forward_amd/ablation.py, fa2_attn_fwd_variant), as
-the reference tests its knockout copy (tests/test_ablation.py:16-48):
+"""The kernel's timing variants (libfa2_ablate.so via triton-fa2-forward_amd/ablation.py), as the
+reference tests its knockout copy (tests/test_ablation.py:16-48):
 
-* with no switch on, the variant entry point is the production kernel, bit for bit;
+* with no switch on, the variant is the production kernel, bit for bit (copy): against
+  attention() where that launches the table-free kernel, and against fa2_attn_fwd on a shape
+  where attention() adds the key-norm pass (there the variants are timed against copy);
 * mask_every_tile only adds work: still bit for bit;
 * scale_first, and both switches together (the reference's "before_fixes"), still compute
-  attention: the 2x-SDPA rule against the fp64 oracle.
-
-The reference's work-skipping switches (no_exp, no_softmax, kv_l2) are not part of this library;
-tests/test_frontend.py checks that asking for them fails.
+  attention: the 2x-SDPA rule against the fp64 oracle;
+* the work-skipping knockouts (no_exp, no_softmax, kv_l2, matmul_only) change the output
+  (tests/test_ablation.py:28-34), on both of the kernel's tile loops (software-pipelined at
+  head_dim 64, one tile at a time otherwise), causal or not.
 """
 
 import pytest
@@ -34,6 +36,18 @@ def test_copy_is_the_production_kernel(causal, pack_gqa, N):
     q, k, v = make_qkv(BATCH, 8, 2, N, N, 64, torch.float16)
     assert torch.equal(_ablate()(q, k, v, causal=causal, pack_gqa=pack_gqa),
                        attention(q, k, v, causal=causal, pack_gqa=pack_gqa))
+
+
+def test_copy_is_the_table_free_launch_where_attention_adds_the_key_norm_pass():
+    """bf16, head_dim 128, causal, N 4096, H 32/8: attention() asks for the key-norm table here
+    (fa2_workspace_bytes_for), the variants never do; copy equals fa2_attn_fwd's launch."""
+    from ablation import table_free_launch
+    from fa2 import _lib
+
+    q, k, v = make_qkv(1, 32, 8, 4096, 4096, 128, torch.bfloat16)
+    assert (_lib.workspace_bytes_for(1, 32, 8, 4096, 4096, 128, q.dtype, True, 1)
+            > _lib.workspace_bytes(1, 32, 4096, 128, 1))
+    assert torch.equal(_ablate()(q, k, v, causal=True), table_free_launch(q, k, v, True))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -67,3 +81,20 @@ def test_scale_first_changes_only_rounding():
     a = _ablate()(q, k, v, causal=True, scale_first=True)
     b = attention(q, k, v, causal=True)
     assert (a.float() - b.float()).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("knobs", [{"no_exp": True}, {"no_softmax": True}, {"kv_l2": True},
+                                   {"no_softmax": True, "kv_l2": True}],
+                         ids=["no_exp", "no_softmax", "kv_l2", "matmul_only"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 16), (torch.bfloat16, 32),
+                                     (torch.float16, 64), (torch.bfloat16, 64),
+                                     (torch.bfloat16, 128)])
+def test_knockouts_change_the_output(knobs, causal, dtype, D):
+    """300 keys span three tiles at every head dim (128-key tiles at 16, 64-key tiles above), so
+    kv_l2's repeated first tile differs from the real ones."""
+    from fa2.kernel import attention
+
+    q, k, v = make_qkv(BATCH, 4, 2, 300, 300, D, dtype)
+    out = _ablate()(q, k, v, causal=causal, **knobs)
+    assert not torch.equal(out, attention(q, k, v, causal=causal))

@@ -1,30 +1,36 @@
-"""Kernel variants for attributing the kernel's time (counterpart of the reference's
-bench/ablation.py). GPU only.
+"""Timing variants of the forward kernel: what each kind of its work costs (the counterpart of the
+reference's bench/ablation.py). GPU only; a measurement tool, not part of the drop-in.
 
-    python triton-fa2-forward_amd/ablation.py                       # N 4096 and 16384, fp16, causal
-    python triton-fa2-forward_amd/ablation.py --seqlens 8192 --dtype bf16 --rounds 5
+    python triton-fa2-forward_amd/ablation.py                          # fp16, N 4096 and 16384, causal
+    python triton-fa2-forward_amd/ablation.py --seqlens 8192 --dtype bf16 --rounds 5       # C3
+    python triton-fa2-forward_amd/ablation.py --seqlens 16384 --batch 2 --hq 16 --hkv 16 \\
+        --head-dim 64 --full --input-scale 0.5 --rounds 5                                    # C4
 
-The reference keeps a copy of its kernel with five switches (bench/ablation.py:1-20). Two of them
-undo the kernel's two instruction-count choices and still compute attention; here they are
-compile-time flags of the one kernel template (attn_fwd_kernel's VARIANT), reached through
-fa2_attn_fwd_variant:
+Every variant is the product's kernel template instantiated with VARIANT bits
+(include/fa2_ablate.h), loaded from the measurement library libfa2_ablate.so, which fa2.kernel
+never loads. The reference's variants (bench/ablation.py:1-20, 42-53):
 
-  scale_first      multiply every score by the scale, then subtract the row max (two VALU
-                   instructions per score) instead of one FMA, s * scale - m
-  mask_every_tile  apply the causal / end-of-sequence mask on every K/V tile, not only on the
-                   tiles that need it
+  copy             no switch: the product kernel, bit for bit the launch of fa2_attn_fwd
+  scale_first      multiply every score by the scale, then subtract the row max
+  mask_every_tile  apply the mask on every K/V tile, not only where needed
+  before_fixes     both of the above
+  no_exp           exp2 replaced by its argument            (output wrong on purpose)
+  no_softmax       no mask, max, exp, sum or rescale        (output wrong on purpose)
+  kv_l2            every tile loads K/V tile 0 again: L2 hits instead of HBM reads
+  matmul_only      no_softmax + kv_l2: the two products and the loads' issue cost
+  pack             copy with GQA head packing forced on
 
-before_fixes turns both on; copy turns neither on and is the production kernel (bit for bit, as
-tests/test_gpu_ablation.py checks); pack forces GQA head packing. The reference's other three
-switches (no_exp, no_softmax, kv_l2) skip work and produce wrong outputs by design. They are not
-part of this library: their numbers come from a separate, unshipped copy of the kernel.
-
-Timing follows the reference (HIP events around every launch, median and IQR) after bench.py's
-1 s clock settle, interleaved over rounds so that clock drift hits every variant alike
-(bench/ablation.py:252-255).
+Measurement (this repository's bench.py harness): the clocks are settled once (bench.settle_clocks);
+then, round after round, every variant runs W warmup launches and K launches back to back between one
+pair of HIP events (bench.time_steps), so that each round yields one ms-per-launch figure per variant
+and clock drift hits all variants alike. The table gives each variant's median over the rounds, the
+spread of its rounds, and the change against `copy`. `attention()` is the shipped call on the same
+inputs; on long bf16 problems it adds the key-norm pass and that instance of the kernel (C3), which
+the variants do not have, so the deltas are taken against `copy`, not against it.
 """
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -35,32 +41,65 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 sys.path.insert(0, os.path.dirname(HERE))
 
-KNOBS = ("scale_first", "mask_every_tile")
-SKIPPING = ("no_exp", "no_softmax", "kv_l2")     # the reference's, not built here
-VARIANTS = {                                       # name -> switches on
+ABLATE_LIB_PATH = os.path.join(HERE, "libfa2_ablate.so")
+
+# switch -> VARIANT bit (FA2_ABLATE_* in include/fa2_ablate.h)
+SWITCH_BITS = {"scale_first": 1, "mask_every_tile": 2, "no_exp": 8, "no_softmax": 16, "kv_l2": 32}
+KNOBS = tuple(SWITCH_BITS)
+VARIANTS = {
     "copy": (),
     "scale_first": ("scale_first",),
     "mask_every_tile": ("mask_every_tile",),
     "before_fixes": ("scale_first", "mask_every_tile"),
-    "pack": ("pack",),                             # the copy with GQA head packing forced on
+    "no_exp": ("no_exp",),
+    "no_softmax": ("no_softmax",),
+    "kv_l2": ("kv_l2",),
+    "matmul_only": ("no_softmax", "kv_l2"),
+    "pack": ("pack",),
 }
-VARIANT_BITS = {"scale_first": 1, "mask_every_tile": 2}   # FA2_VARIANT_* in include/fa2_fwd.h
+# variants whose output must equal the product's bit for bit (the others change rounding or are
+# wrong by design)
+EXACT = ("copy", "mask_every_tile", "pack")
+
+_LIB = None
+
+
+def ablate_lib():
+    """libfa2_ablate.so, loaded on first use (after torch, which brings the HIP runtime)."""
+    global _LIB
+    if _LIB is None:
+        import torch  # noqa: F401
+
+        if not os.path.exists(ABLATE_LIB_PATH):
+            raise RuntimeError(f"{ABLATE_LIB_PATH} is missing; build it with "
+                               "python triton-fa2-forward_amd/csrc/build.py")
+        lib = ctypes.CDLL(ABLATE_LIB_PATH)
+        i32, i64p, vp = ctypes.c_int32, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p
+        lib.fa2_ablate_attn_fwd.restype = ctypes.c_int
+        lib.fa2_ablate_attn_fwd.argtypes = [vp, vp, vp, vp, i64p, i64p, i64p, i64p] + [i32] * 9 + \
+            [ctypes.c_float, i32, vp]
+        lib.fa2_ablate_last_error.restype = ctypes.c_char_p
+        lib.fa2_ablate_last_error.argtypes = []
+        _LIB = lib
+    return _LIB
+
+
+def variant_bits(switches):
+    unknown = set(switches) - set(SWITCH_BITS)
+    assert not unknown, f"unknown switches {sorted(unknown)}"
+    return sum(SWITCH_BITS[s] for s in switches)
 
 
 def attention_ablate(q, k, v, causal=True, pack_gqa=False, **knobs):
-    """fa2.kernel.attention at the default configuration with the switches in KNOBS
-    (bench/ablation.py:182-200). Same argument rules as attention()."""
+    """fa2.kernel.attention at the default configuration with the switches in KNOBS turned on
+    (the reference's attention_ablate signature, bench/ablation.py:182-200); the argument rules are
+    attention()'s."""
     import torch
 
     from fa2 import _lib
     from fa2.kernel import LOG2E, _default_config, _loadable
 
-    skipping = sorted(set(knobs) & set(SKIPPING))
-    if skipping:
-        raise ValueError(f"switches {skipping} skip work and are not built into this library "
-                         "(their timings come from an unshipped copy of the kernel)")
-    unknown = set(knobs) - set(KNOBS)
-    assert not unknown, f"unknown switches {sorted(unknown)}"
+    bits = variant_bits([name for name, on in knobs.items() if on])
     assert q.dim() == k.dim() == v.dim() == 4
     B, H_q, N_q, D = q.shape
     H_kv, N_kv = k.shape[1], k.shape[2]
@@ -70,96 +109,156 @@ def attention_ablate(q, k, v, causal=True, pack_gqa=False, **knobs):
     assert D in (16, 32, 64, 128), "head_dim must be a power of two in [16, 128]"
     if causal:
         assert N_q == N_kv, "causal attention here assumes N_q == N_kv"
-    bm = _default_config(D, True)[0]
     group = H_q // H_kv
-    if pack_gqa and bm % group:
-        raise ValueError(f"pack_gqa needs BLOCK_M ({bm}) to be a multiple of the GQA group ({group})")
+    block_m = _default_config(D, True)[0]
+    if pack_gqa and block_m % group:
+        raise ValueError(f"pack_gqa needs BLOCK_M ({block_m}) to be a multiple of the GQA group ({group})")
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise RuntimeError("attention_ablate runs on the GPU; got CPU tensors")
-    variant = sum(VARIANT_BITS[kn] for kn, on in knobs.items() if on)
     out = torch.empty_like(q)
     if out.numel() == 0:
         return out
     q_, k_, v_, o_ = _loadable(q), _loadable(k), _loadable(v), _loadable(out)
+    lib = ablate_lib()
     with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        _lib.attn_fwd_variant(q_, k_, v_, o_, causal, group if pack_gqa else 1,
-                              1.0 / math.sqrt(D) * LOG2E, variant, stream)
+        rc = lib.fa2_ablate_attn_fwd(
+            q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o_.data_ptr(), _lib._strides(q_),
+            _lib._strides(k_), _lib._strides(v_), _lib._strides(o_), B, H_q, H_kv, N_q, N_kv, D,
+            _lib.DTYPE_CODE[q.dtype], int(bool(causal)), group if pack_gqa else 1,
+            LOG2E / math.sqrt(D), bits, torch.cuda.current_stream(q.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"fa2_ablate_attn_fwd failed ({rc}): "
+                           f"{lib.fa2_ablate_last_error().decode(errors='replace')}")
     if o_ is not out:
         out.copy_(o_)
     return out
 
 
-def _summarize(ms):
-    q1, med, q3 = statistics.quantiles(ms, n=4, method="inclusive")
-    return {"median_ms": med, "iqr_ms": q3 - q1}
+def table_free_launch(q, k, v, causal):
+    """fa2_attn_fwd at the default configuration: the product kernel without the key-norm table,
+    which is what `copy` must equal bit for bit."""
+    import torch
+
+    from fa2 import _lib
+    from fa2.kernel import LOG2E
+
+    out = torch.empty_like(q)
+    _lib.attn_fwd(q, k, v, out, causal, 1, 128, 0, LOG2E / math.sqrt(q.shape[3]),
+                  torch.cuda.current_stream().cuda_stream)
+    return out
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--seqlens", type=int, nargs="+", default=[4096, 16384])
-    ap.add_argument("--hq", type=int, default=32)
-    ap.add_argument("--hkv", type=int, default=8)
-    ap.add_argument("--head-dim", type=int, default=128)
-    ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--iters", type=int, default=20)
-    ap.add_argument("--variants", nargs="+", default=list(VARIANTS), choices=list(VARIANTS))
-    ap.add_argument("--rounds", type=int, default=3, help="interleaved rounds; samples are pooled")
-    ap.add_argument("--json", default=None)
-    args = ap.parse_args()
+def launcher(name, q, k, v, causal):
+    switches = [s for s in VARIANTS[name] if s != "pack"]
+    pack = "pack" in VARIANTS[name]
+    return lambda: attention_ablate(q, k, v, causal=causal, pack_gqa=pack,
+                                    **{s: True for s in switches})
 
+
+def interleaved_rounds(launchers, rounds, steps, warmup):
+    """{name: [ms per launch, one per round]}: bench.time_steps per variant, variants interleaved."""
+    import bench
+
+    per_round = {name: [] for name in launchers}
+    for _ in range(rounds):
+        for name, fn in launchers.items():
+            total_ms, _ = bench.time_steps(fn, steps, warmup)
+            per_round[name].append(total_ms / steps)
+    return per_round
+
+
+def measure_shape(args, N):
     import torch
 
     import bench
     from fa2.kernel import attention
 
     dtype = {"fp16": torch.float16, "bf16": torch.bfloat16}[args.dtype]
+    causal = not args.full
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q, k, v = (torch.randn(args.batch, h, N, args.head_dim, generator=g) * args.input_scale
+               for h in (args.hq, args.hkv, args.hkv))
+    q, k, v = (t.to(dtype).cuda() for t in (q, k, v))
+    flops = bench.attn_flops(args.batch, args.hq, N, N, args.head_dim, causal)
+
+    product = table_free_launch(q, k, v, causal)
+    shipped = attention(q, k, v, causal=causal)
+    launchers = {"attention()": lambda: attention(q, k, v, causal=causal)}
+    outputs = {}
+    for name in args.variants:
+        launchers[name] = launcher(name, q, k, v, causal)
+        outputs[name] = launchers[name]()
+    torch.cuda.synchronize()
+    checks = {}
+    for name, out in outputs.items():
+        diff = (out.float() - product.float()).abs().max().item()
+        checks[name] = {"bit_exact": bool(torch.equal(out, product)), "max_abs_diff": diff}
+        if name in EXACT and not checks[name]["bit_exact"]:
+            raise SystemExit(f"variant {name} differs from the product kernel (max diff {diff:.3e})")
+    checks["attention()"] = {"bit_exact": bool(torch.equal(shipped, product)),
+                             "max_abs_diff": (shipped.float() - product.float()).abs().max().item()}
+
+    bench.settle_clocks(launchers["copy"] if "copy" in launchers else launchers["attention()"])
+    per_round = interleaved_rounds(launchers, args.rounds, args.steps, args.warmup)
+    base = statistics.median(per_round["copy"]) if "copy" in per_round else None
     rows = []
+    for name, ms in per_round.items():
+        med = statistics.median(ms)
+        rows.append({"variant": name, "ms": med, "min_ms": min(ms), "max_ms": max(ms),
+                     "vs_copy": (med / base - 1.0) if base else None,
+                     "tflops": flops / (med * 1e-3) / 1e12, **checks.get(name, {})})
+    del q, k, v, product, shipped, outputs
+    torch.cuda.empty_cache()
+    return flops, rows
+
+
+def print_table(args, N, rows):
+    shape = (f"B={args.batch} H {args.hq}/{args.hkv} N={N} D={args.head_dim} {args.dtype} "
+             f"{'full' if args.full else 'causal'}" + (f" inputs x{args.input_scale}" if args.input_scale != 1 else ""))
+    print(f"\n{shape}: {args.rounds} rounds of {args.steps} back-to-back launches per variant")
+    print("| variant | ms per launch (median; min-max over rounds) | vs copy | TFLOP/s | output vs product |")
+    print("|---|---|---|---|---|")
+    for r in rows:
+        if r.get("bit_exact"):
+            out = "bit-exact"
+        elif "max_abs_diff" in r:
+            out = f"max diff {r['max_abs_diff']:.2e}"
+        else:
+            out = ""
+        vs = "" if r["vs_copy"] is None or r["variant"] == "copy" else f"{r['vs_copy']:+.1%}"
+        print(f"| {r['variant']} | {r['ms']:.4f} ({r['min_ms']:.4f}-{r['max_ms']:.4f}) | {vs} | "
+              f"{r['tflops']:.1f} | {out} |", flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description="timing variants of the forward kernel")
+    ap.add_argument("--seqlens", type=int, nargs="+", default=[4096, 16384])
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--hq", type=int, default=32)
+    ap.add_argument("--hkv", type=int, default=8)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
+    ap.add_argument("--full", action="store_true", help="no causal mask")
+    ap.add_argument("--input-scale", type=float, default=1.0, help="q, k, v ~ N(0, 1) times this")
+    ap.add_argument("--variants", nargs="+", default=list(VARIANTS), choices=list(VARIANTS))
+    ap.add_argument("--rounds", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20, help="back-to-back launches per variant per round")
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--json", default=None, help="also write the rows here")
+    args = ap.parse_args()
+
+    import torch
+
+    if not torch.cuda.is_available():
+        raise SystemExit("ablation.py needs the GPU")
+    results = []
     for N in args.seqlens:
-        g = torch.Generator(device="cpu").manual_seed(0)
-        q = torch.randn(1, args.hq, N, args.head_dim, generator=g).to("cuda", dtype)
-        k = torch.randn(1, args.hkv, N, args.head_dim, generator=g).to("cuda", dtype)
-        v = torch.randn(1, args.hkv, N, args.head_dim, generator=g).to("cuda", dtype)
-        flops = bench.attn_flops(1, args.hq, N, N, args.head_dim, True)
-        ref = attention(q, k, v, causal=True)
-        fns = {"production": lambda: attention(q, k, v, causal=True)}
-        info = {}
-        for name in args.variants:
-            knobs = {kn: True for kn in VARIANTS[name] if kn != "pack"}
-            fn = (lambda knobs=knobs, pack="pack" in VARIANTS[name]:
-                  attention_ablate(q, k, v, causal=True, pack_gqa=pack, **knobs))
-            out = fn()
-            info[name] = dict(bit_exact=torch.equal(out, ref),
-                              max_abs_diff=(out.float() - ref.float()).abs().max().item())
-            fns[name] = fn
-        bench.settle_clocks(fns["production"])
-        samples = {name: [] for name in fns}
-        for _ in range(args.rounds):
-            for name, fn in fns.items():
-                for _ in range(args.warmup):
-                    fn()
-                samples[name] += bench.time_each(fn, args.iters)
-        base = _summarize(samples["production"])
-        print(f"\nN={N} {args.dtype} H {args.hq}/{args.hkv} D {args.head_dim} causal  "
-              f"(production {base['median_ms']:.3f} ms, {flops / base['median_ms'] / 1e9:.1f} TFLOP/s)")
-        print("| variant | ms (IQR) | vs production | TFLOP/s | output |")
-        print("|---|---|---|---|---|")
-        for name in fns:
-            s = _summarize(samples[name])
-            delta = s["median_ms"] - base["median_ms"]
-            out = ("" if name == "production" else "bit-exact" if info[name]["bit_exact"]
-                   else f"max diff {info[name]['max_abs_diff']:.2e}")
-            print(f"| {name} | {s['median_ms']:.3f} ({s['iqr_ms']:.3f}) | {delta:+.3f} "
-                  f"({delta / base['median_ms']:+.1%}) | {flops / s['median_ms'] / 1e9:.1f} | {out} |",
-                  flush=True)
-            rows.append(dict(seqlen=N, variant=name, rounds=args.rounds, **s,
-                             **info.get(name, {})))
-        del q, k, v, ref
-        torch.cuda.empty_cache()
+        flops, rows = measure_shape(args, N)
+        print_table(args, N, rows)
+        results.append({"seqlen": N, "flops": flops, "rows": rows})
     if args.json:
         with open(args.json, "w") as f:
-            json.dump({"config": vars(args), "results": rows}, f, indent=1)
+            json.dump({"args": vars(args), "results": results}, f, indent=1)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,49 @@
+// attn_fwd_ablate_inst.hip - the timing-variant instances of one (dtype, head_dim) pair for the
+// measurement library. Compiled once per pair with -DFA2_DT=<0|1> -DFA2_D=<16|32|64|128>.
+#include "attn_fwd_ablate.hpp"
+#include "attn_fwd_kernel.hpp"
+#include "attn_fwd_launch.hpp"
+
+#if !defined(FA2_DT) || !defined(FA2_D)
+#error "compile with -DFA2_DT=<0|1> -DFA2_D=<16|32|64|128>"
+#endif
+
+namespace fa2 {
+
+namespace {
+
+template <int DT, int D, int VARIANT>
+int launch_variant(const Params& p, bool causal, unsigned grid, hipStream_t s) {
+  constexpr int BN = default_block_n(D);
+  if (causal)
+    hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, VARIANT>), dim3(grid), dim3(256), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, VARIANT>), dim3(grid), dim3(256), 0,
+                       s, p);
+  return (int)hipGetLastError();
+}
+
+template <int DT, int D, int... V>
+int dispatch(const Params& p, int variant, bool causal, unsigned grid, hipStream_t s) {
+  int rc = (int)hipErrorInvalidValue;
+  (void)((variant == V ? (rc = launch_variant<DT, D, V>(p, causal, grid, s), true) : false) || ...);
+  return rc;
+}
+
+}  // namespace
+
+template <int DT, int D>
+int launch_attn_fwd_ablate(const Params& p, int variant, bool causal, unsigned grid,
+                           hipStream_t s) {
+  return dispatch<DT, D, kAblationVariants[0], kAblationVariants[1], kAblationVariants[2],
+                  kAblationVariants[3], kAblationVariants[4], kAblationVariants[5],
+                  kAblationVariants[6], kAblationVariants[7]>(p, variant, causal, grid, s);
+}
+
+static_assert(sizeof(kAblationVariants) / sizeof(int) == 8, "dispatch lists every variant");
+
+template int launch_attn_fwd_ablate<FA2_DT, FA2_D>(const Params&, int, bool, unsigned,
+                                                   hipStream_t);
+
+}  // namespace fa2

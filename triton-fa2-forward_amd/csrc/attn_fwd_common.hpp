@@ -49,6 +49,12 @@ constexpr int kVariantMaskEveryTile = 2;
 // Not a timing variant: the instance that reads the key-norm table and skips the row max where
 // the table proves it unneeded (launched by the production path when a table was written).
 constexpr int kVariantKeyBound = 4;
+// Work-skipping knockouts, built only into the measurement library (fa2_ablate.hip), never into
+// the product: the reference's ablation switches that remove one kind of work so that its cost is
+// the time difference (bench/ablation.py:6-10). Their outputs are wrong by design.
+constexpr int kVariantNoExp = 8;       // exp2 replaced by its argument (alpha too)
+constexpr int kVariantNoSoftmax = 16;  // no mask, row max, exp, sum or rescale: O = (Q K^T) V
+constexpr int kVariantKvL2 = 32;       // every tile loads the first K/V tile again (L2 hits)
 
 // ---------------------------------------------------------------------------------
 // element type traits: the MFMA, the fp32 -> 16-bit pair conversion (RNE) and the fp32 sum of

@@ -53,24 +53,6 @@ int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsign
   }
 }
 
-template <int DT, int D>
-int launch_attn_fwd_variant(const Params& p, int variant, bool causal, unsigned grid,
-                            hipStream_t s) {
-  constexpr int BN = default_block_n(D);
-  switch (variant * 2 + (causal ? 1 : 0)) {
-    case 0: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, 0>), dim3(grid), dim3(256), 0, s, p); break;
-    case 1: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, 0>), dim3(grid), dim3(256), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, 1>), dim3(grid), dim3(256), 0, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, 1>), dim3(grid), dim3(256), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, 2>), dim3(grid), dim3(256), 0, s, p); break;
-    case 5: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, 2>), dim3(grid), dim3(256), 0, s, p); break;
-    case 6: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, 3>), dim3(grid), dim3(256), 0, s, p); break;
-    default: hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, 3>), dim3(grid), dim3(256), 0, s, p); break;
-  }
-  return (int)hipGetLastError();
-}
-
 template int launch_attn_fwd<FA2_DT, FA2_D>(const Params&, int, int, bool, unsigned, hipStream_t);
-template int launch_attn_fwd_variant<FA2_DT, FA2_D>(const Params&, int, bool, unsigned, hipStream_t);
 
 }  // namespace fa2

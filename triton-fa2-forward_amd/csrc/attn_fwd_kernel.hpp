@@ -47,11 +47,13 @@ namespace fa2 {
 // ---------------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------------
-// VARIANT is 0 for the product. Its bits turn on the two instruction-count choices the
-// reference's ablation undoes (bench/ablation.py:11-17), for timing them against the product:
+// VARIANT is 0 for the product (kVariantKeyBound for its key-norm instance). The measurement
+// library instantiates the timing variants of the reference's ablation (bench/ablation.py:1-20):
 // kVariantScaleFirst scales every score before the row max and subtracts the max separately
 // (two VALU instructions per score instead of one FMA); kVariantMaskEveryTile applies the mask
-// on every K/V tile, not only on the tiles that need it. Both compute the same attention.
+// on every K/V tile, not only on the tiles that need it (both still compute attention); and the
+// knockouts kVariantNoExp, kVariantNoSoftmax and kVariantKvL2, which skip work and compute
+// garbage on purpose (their time is the point). With none of these bits the code is unchanged.
 //
 // Register budget: two waves per SIMD (256 VGPRs each), except for the software-pipelined loop
 // (head_dim 64, 64- or 32-key tiles), which is held to three (168 VGPRs): measured +4.5-5.5% for
@@ -64,6 +66,11 @@ void attn_fwd_kernel(const Params p) {
   constexpr bool kScaleFirst = (VARIANT & kVariantScaleFirst) != 0;
   constexpr bool kMaskEveryTile = (VARIANT & kVariantMaskEveryTile) != 0;
   constexpr bool KB = (VARIANT & kVariantKeyBound) != 0;  // key-norm table present
+  constexpr bool kNoExp = (VARIANT & kVariantNoExp) != 0;
+  constexpr bool kNoSoftmax = (VARIANT & kVariantNoSoftmax) != 0;
+  constexpr bool kKvL2 = (VARIANT & kVariantKvL2) != 0;
+  // exp2, or (knockout) its argument
+  auto ex2 = [](float x) { return kNoExp ? x : __builtin_amdgcn_exp2f(x); };
   constexpr int KS = D / 16;               // 16-dim k-steps of S^T = K Q^T
   constexpr int DB = (D + 31) / 32;        // 32-dim row blocks of O^T
   constexpr int NB = BN / 32;              // 32-key row blocks of S^T
@@ -197,7 +204,7 @@ void attn_fwd_kernel(const Params p) {
     return make_desc(base + (int64_t)n0 * stride * 2, (uint32_t)min(bytes, (int64_t)0x7fffffff));
   };
   auto issue_k = [&](int n0, int buf) {
-    const auto rs = rsrc_at(kbase, p.skn, n0);
+    const auto rs = rsrc_at(kbase, p.skn, kKvL2 ? kv_begin : n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
       const int j = wave + jj * NW;
@@ -205,7 +212,7 @@ void attn_fwd_kernel(const Params p) {
     }
   };
   auto issue_v = [&](int n0, int buf) {
-    const auto rs = rsrc_at(vbase, p.svn, n0);
+    const auto rs = rsrc_at(vbase, p.svn, kKvL2 ? kv_begin : n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
       const int j = wave + jj * NW;
@@ -367,7 +374,7 @@ void attn_fwd_kernel(const Params p) {
       // masks (fa2/kernel.py:81-88): key n is visible iff n < n_kv and (causal) n <= pos. The
       // condition is uniform over the workgroup (a scalar branch), and one copy of the tile code
       // serves masked and unmasked tiles so the accumulators keep one register assignment.
-      if (kMaskEveryTile || n0 + BN > full_end) {
+      if (!kNoSoftmax && (kMaskEveryTile || n0 + BN > full_end)) {
         const int lim = (CAUSAL ? min(pos_vis, p.n_kv - 1) : p.n_kv - 1) - n0 - 8 * g;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -380,7 +387,7 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) s[nb] *= qk_scale;
       }
-      if (!KB || !skip_max) {
+      if (!kNoSoftmax && (!KB || !skip_max)) {
         float mx = -INFINITY;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -390,7 +397,7 @@ void attn_fwd_kernel(const Params p) {
         const bool grow = !skip_row && mx > m_i + kRescaleTau;
         if (__builtin_amdgcn_ballot_w64(grow)) {
           const float m_new = grow ? mx : m_i;
-          const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+          const float alpha = ex2(m_i - m_new);
           l_i *= alpha;
           l_exact *= alpha;
 #pragma unroll
@@ -402,16 +409,17 @@ void attn_fwd_kernel(const Params p) {
           skip_max = __builtin_amdgcn_ballot_w64(!skip_row) == 0;
         }
       }
+      if constexpr (!kNoSoftmax) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          s[nb][i] = __builtin_amdgcn_exp2f(kScaleFirst ? s[nb][i] - m_i
-                                                        : __builtin_fmaf(s[nb][i], qk_scale, -m_i));
-      if constexpr (!kRoundedSum) {
-        l_i += lane_sum(s);
-      } else if (want_exact) {
-        l_exact += lane_sum(s);
+          for (int i = 0; i < 16; ++i)
+            s[nb][i] = ex2(kScaleFirst ? s[nb][i] - m_i : __builtin_fmaf(s[nb][i], qk_scale, -m_i));
+        if constexpr (!kRoundedSum) {
+          l_i += lane_sum(s);
+        } else if (want_exact) {
+          l_exact += lane_sum(s);
+        }
       }
 
       // O^T += V^T P^T with P rounded to the input type (fa2/kernel.py:100-105)
@@ -424,7 +432,7 @@ void attn_fwd_kernel(const Params p) {
                       E::pack2(s[nb][8 * h + 4], s[nb][8 * h + 5]),
                       E::pack2(s[nb][8 * h + 6], s[nb][8 * h + 7])};
       }
-      if constexpr (kRoundedSum) {
+      if constexpr (kRoundedSum && !kNoSoftmax) {
         float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
         for (int t = 0; t < BN / 16; ++t) {
@@ -511,6 +519,10 @@ void attn_fwd_kernel(const Params p) {
     };
     // the new reference max (fa2/kernel.py:95), lazily moved; returns whether it moved
     auto row_max = [&](f32x16 (&sv)[NB]) {
+      if constexpr (kNoSoftmax) {
+        m_new = m_i;
+        return false;
+      }
       if constexpr (kScaleFirst) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) sv[nb] *= qk_scale;
@@ -527,14 +539,15 @@ void attn_fwd_kernel(const Params p) {
     };
     // P = exp2(S * scale - m) rounded to the input type, and l (fa2/kernel.py:96-98, 105)
     auto softmax_p = [&](f32x16 (&sv)[NB], u32x4 (&pb)[NT]) {
+      if constexpr (!kNoSoftmax) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          sv[nb][i] = __builtin_amdgcn_exp2f(
-              kScaleFirst ? sv[nb][i] - m_i : __builtin_fmaf(sv[nb][i], qk_scale, -m_i));
-      if constexpr (!kRoundedSum) {
-        l_i += lane_sum(sv);
+          for (int i = 0; i < 16; ++i)
+            sv[nb][i] = ex2(kScaleFirst ? sv[nb][i] - m_i : __builtin_fmaf(sv[nb][i], qk_scale, -m_i));
+        if constexpr (!kRoundedSum) {
+          l_i += lane_sum(sv);
+        }
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -544,7 +557,7 @@ void attn_fwd_kernel(const Params p) {
                       E::pack2(sv[nb][8 * h + 4], sv[nb][8 * h + 5]),
                       E::pack2(sv[nb][8 * h + 6], sv[nb][8 * h + 7])};
       }
-      if constexpr (kRoundedSum) {
+      if constexpr (kRoundedSum && !kNoSoftmax) {
         float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -571,7 +584,7 @@ void attn_fwd_kernel(const Params p) {
       }
     };
     auto rescale = [&]() {
-      const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+      const float alpha = ex2(m_i - m_new);
       l_i *= alpha;
       l_exact *= alpha;
 #pragma unroll
@@ -609,7 +622,7 @@ void attn_fwd_kernel(const Params p) {
       __syncthreads();  // every wave's; every wave is done with K_{j+1} and V_{j-1}
       if (j + 3 < n_tiles_kv) issue_k(kv_begin + (j + 3) * BN, bufk);
       issue_v(n1, bufv ^ 1);
-      if (kMaskEveryTile || n1 + BN > full_end) mask_s(s_nxt, n1);
+      if (!kNoSoftmax && (kMaskEveryTile || n1 + BN > full_end)) mask_s(s_nxt, n1);
 
       // block B: PV_j with the row max of S_{j+1} and K_{j+2}'s first operands in between
       u32x4 va[LA_V];
@@ -655,7 +668,7 @@ void attn_fwd_kernel(const Params p) {
       wait_vmcnt<0>();
       __syncthreads();  // V_0 and K_1 have landed; every wave is done with K_0
       if (n_tiles_kv > 2) issue_k(kv_begin + 2 * BN, 0);
-      if (kMaskEveryTile || kv_begin + BN > full_end) mask_s(s_a, kv_begin);
+      if (!kNoSoftmax && (kMaskEveryTile || kv_begin + BN > full_end)) mask_s(s_a, kv_begin);
       row_max(s_a);
       m_i = m_new;  // O and l are still zero
       if constexpr (KB) {
@@ -696,7 +709,8 @@ void attn_fwd_kernel(const Params p) {
   }
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
-  const float l = pair_sum(l_i);
+  // (knockout without softmax: l = 1, as the reference's l_i + 1 on a zero sum)
+  const float l = kNoSoftmax ? 1.0f : pair_sum(l_i);
   const float lx = want_exact ? pair_sum(l_exact) : l;
   // one division per row, then multiplies: a per-element fp32 division expands to ~11 VALU
   // instructions (64 per lane at head_dim 128, ~1.6 us per wave in every program's epilogue)

@@ -22,12 +22,6 @@ int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsign
 // +3.6% full on a B2 H16 N16384 shape).
 constexpr int default_block_n(int head_dim) { return head_dim == 16 ? 128 : 64; }
 
-// Launches attn_fwd_kernel<DT, D, 4, default_block_n(D), causal, variant> (128 rows per
-// program), variant in [0, 3]: the timing variants of the product kernel.
-template <int DT, int D>
-int launch_attn_fwd_variant(const Params& p, int variant, bool causal, unsigned grid,
-                            hipStream_t stream);
-
 // Launches the split-KV combine pass (attn_fwd_combine.hip).
 int launch_combine(int dtype, int head_dim, const CombineParams& c, hipStream_t stream);
 
@@ -37,9 +31,7 @@ int launch_key_norm(int dtype, int head_dim, const KeyNormParams& k, unsigned gr
 
 #define FA2_DECLARE_LAUNCH(DT, D)                                                          \
   extern template int launch_attn_fwd<DT, D>(const Params&, int, int, bool, unsigned, \
-                                             hipStream_t);                              \
-  extern template int launch_attn_fwd_variant<DT, D>(const Params&, int, bool, unsigned, \
-                                                     hipStream_t);
+                                             hipStream_t);
 FA2_DECLARE_LAUNCH(0, 16)
 FA2_DECLARE_LAUNCH(0, 32)
 FA2_DECLARE_LAUNCH(0, 64)

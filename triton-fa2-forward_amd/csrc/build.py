@@ -1,4 +1,5 @@
-"""Build libfa2_fwd.so, the gfx950 FlashAttention-2 forward library, in-tree.
+"""Build libfa2_fwd.so, the gfx950 FlashAttention-2 forward library, in-tree, and the
+measurement library libfa2_ablate.so beside it.
 
     python triton-fa2-forward_amd/csrc/build.py [-j 8] [--verbose]
 
@@ -7,10 +8,22 @@ Compiles attn_fwd_inst.hip once per (dtype, head_dim) pair plus the split-KV com
 in parallel, with hipcc for gfx950 only, and links them into
 triton-fa2-forward_amd/fa2/libfa2_fwd.so next to the Python front end that loads it. Then builds
 the plain-C host of the C ABI that the tests run (tests/capi/fa2_capi_check).
+
+The measurement library (include/fa2_ablate.h) is the kernel's timing variants: the same kernel
+template with work switched off, compiled from attn_fwd_ablate_inst.hip per pair and linked with
+its own C-ABI file fa2_ablate.hip into triton-fa2-forward_amd/libfa2_ablate.so, outside the
+fa2 package: the product never loads it.
+
+Both libraries are built with hidden visibility, so each exports exactly the functions its
+header declares (FA2_API). The compiler's resource report for every kernel instance (VGPRs,
+AGPRs, SGPRs, spills, LDS, occupancy; -Rpass-analysis=kernel-resource-usage) is saved to
+triton-fa2-forward_amd/fa2/kernel_resources.json, which sweep.py prints beside its timings.
 """
 
 import argparse
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -22,6 +35,8 @@ ROOT = os.path.dirname(PKG)
 INCLUDE = os.path.join(ROOT, "include")
 OBJ_DIR = os.path.join(PKG, "build", "obj")
 LIB_PATH = os.path.join(PKG, "fa2", "libfa2_fwd.so")
+ABLATE_LIB_PATH = os.path.join(PKG, "libfa2_ablate.so")
+RESOURCES_PATH = os.path.join(PKG, "fa2", "kernel_resources.json")
 CAPI_DIR = os.path.join(ROOT, "tests", "capi")
 
 ARCH = "gfx950"
@@ -38,7 +53,7 @@ def hipcc():
 
 def common_flags():
     return [
-        f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC",
+        f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-fvisibility=hidden",
         # no packed fp32 VALU ops (v_pk_*_f32) anywhere in device code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", CSRC, "-I", INCLUDE,
@@ -46,6 +61,7 @@ def common_flags():
 
 
 def _run(cmd, verbose):
+    """Run one build command; returns its stderr (without the host pass's noise)."""
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -55,27 +71,80 @@ def _run(cmd, verbose):
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+    return err
+
+
+_REMARK = re.compile(r"remark:\s+(Function Name|TotalSGPRs|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|"
+                     r"Occupancy \[waves/SIMD\]|SGPRs Spill|VGPRs Spill|LDS Size \[bytes/block\]):"
+                     r"\s+(\S+)")
+_FIELDS = {"TotalSGPRs": "sgprs", "VGPRs": "vgprs", "AGPRs": "agprs",
+           "ScratchSize [bytes/lane]": "scratch_bytes_per_lane", "Occupancy [waves/SIMD]": "waves_per_simd",
+           "SGPRs Spill": "sgpr_spills", "VGPRs Spill": "vgpr_spills", "LDS Size [bytes/block]": "lds_bytes"}
+_KERNEL = re.compile(r"^_ZN3fa215attn_fwd_kernelILi(\d)ELi(\d+)ELi(\d)ELi(\d+)ELb([01])ELi(\d+)EEEvNS_6ParamsE$")
+
+
+def parse_resources(stderr):
+    """kernel-resource-usage remarks -> {mangled name: {field: int}} for the forward kernel."""
+    out, cur = {}, None
+    for m in _REMARK.finditer(stderr):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {}) if _KERNEL.match(val) else None
+        elif cur is not None:
+            cur[_FIELDS[key]] = int(val)
+    return out
+
+
+def describe_instance(name):
+    """attn_fwd_kernel<DT, D, NW, BN, CAUSAL, VARIANT> template arguments of a mangled name."""
+    m = _KERNEL.match(name)
+    dt, d, nw, bn, causal, variant = (int(x) for x in m.groups())
+    return {"dtype": ("fp16", "bf16")[dt], "head_dim": d, "waves": nw, "block_m": 32 * nw,
+            "block_n": bn, "causal": bool(causal), "variant": variant}
 
 
 def build(jobs=8, verbose=False):
-    """Compile every kernel instance and link the library. Returns the .so path."""
+    """Compile every kernel instance and link both libraries. Returns the product .so path."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     cc = hipcc()
-    units = []
+    units, ablate_units = [], []
     for dt in DTYPES:
         for d in HEAD_DIMS:
             obj = os.path.join(OBJ_DIR, f"attn_fwd_dt{dt}_d{d}.o")
-            units.append([cc, *common_flags(), f"-DFA2_DT={dt}", f"-DFA2_D={d}", "-c",
+            units.append([cc, *common_flags(), "-Rpass-analysis=kernel-resource-usage",
+                          f"-DFA2_DT={dt}", f"-DFA2_D={d}", "-c",
                           os.path.join(CSRC, "attn_fwd_inst.hip"), "-o", obj])
-    for name in ("attn_fwd_combine", "attn_key_norm", "fa2_fwd"):
-        units.append([cc, *common_flags(), "-c", os.path.join(CSRC, name + ".hip"),
-                      "-o", os.path.join(OBJ_DIR, name + ".o")])
+            obj = os.path.join(OBJ_DIR, f"attn_fwd_ablate_dt{dt}_d{d}.o")
+            ablate_units.append([cc, *common_flags(), f"-DFA2_DT={dt}", f"-DFA2_D={d}", "-c",
+                                 os.path.join(CSRC, "attn_fwd_ablate_inst.hip"), "-o", obj])
+    shared = []
+    for name in ("attn_fwd_combine", "attn_key_norm"):
+        shared.append([cc, *common_flags(), "-c", os.path.join(CSRC, name + ".hip"),
+                       "-o", os.path.join(OBJ_DIR, name + ".o")])
+    api = [cc, *common_flags(), "-c", os.path.join(CSRC, "fa2_fwd.hip"),
+           "-o", os.path.join(OBJ_DIR, "fa2_fwd.o")]
+    ablate_api = [cc, *common_flags(), "-c", os.path.join(CSRC, "fa2_ablate.hip"),
+                  "-o", os.path.join(OBJ_DIR, "fa2_ablate.o")]
+    everything = units + shared + [api] + ablate_units + [ablate_api]
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        list(ex.map(lambda cmd: _run(cmd, verbose), units))
-    objs = [u[-1] for u in units]
-    tmp = LIB_PATH + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
-    os.replace(tmp, LIB_PATH)
+        errs = list(ex.map(lambda cmd: _run(cmd, verbose), everything))
+
+    resources = {}
+    for err in errs[:len(units)]:
+        for name, fields in parse_resources(err).items():
+            resources[name] = {**describe_instance(name), **fields}
+    with open(RESOURCES_PATH + ".tmp", "w") as f:
+        json.dump({"arch": ARCH, "source": "hipcc -Rpass-analysis=kernel-resource-usage",
+                   "kernels": dict(sorted(resources.items()))}, f, indent=1)
+    os.replace(RESOURCES_PATH + ".tmp", RESOURCES_PATH)
+
+    def link(objs, path):
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", path + ".tmp", *objs], verbose)
+        os.replace(path + ".tmp", path)
+
+    shared_objs = [u[-1] for u in shared]
+    link([u[-1] for u in units] + shared_objs + [api[-1]], LIB_PATH)
+    link([u[-1] for u in ablate_units] + shared_objs + [ablate_api[-1]], ABLATE_LIB_PATH)
     build_capi_check(verbose)
     return LIB_PATH
 

@@ -1,0 +1,50 @@
+// fa2_ablate.hip - C ABI of the measurement library libfa2_ablate.so (include/fa2_ablate.h):
+// the forward kernel's timing variants behind the same argument checks and launch sequence as
+// the product (attn_fwd_host.hpp, compiled into this library separately).
+#include <hip/hip_runtime.h>
+
+#include "attn_fwd_ablate.hpp"
+#include "attn_fwd_host.hpp"
+#include "fa2_ablate.h"
+
+namespace {
+
+int launch_ablate(int dtype, int di, const Params& p, int waves, int block_n, bool causal,
+                  unsigned grid, hipStream_t s, int variant) {
+  // the variants exist at the default configuration only (4 waves of 32 rows, the default tile)
+  if (waves != 4 || block_n != default_block_n(kDims[di])) return (int)hipErrorInvalidValue;
+  switch (dtype * 4 + di) {
+    case 0: return fa2::launch_attn_fwd_ablate<0, 16>(p, variant, causal, grid, s);
+    case 1: return fa2::launch_attn_fwd_ablate<0, 32>(p, variant, causal, grid, s);
+    case 2: return fa2::launch_attn_fwd_ablate<0, 64>(p, variant, causal, grid, s);
+    case 3: return fa2::launch_attn_fwd_ablate<0, 128>(p, variant, causal, grid, s);
+    case 4: return fa2::launch_attn_fwd_ablate<1, 16>(p, variant, causal, grid, s);
+    case 5: return fa2::launch_attn_fwd_ablate<1, 32>(p, variant, causal, grid, s);
+    case 6: return fa2::launch_attn_fwd_ablate<1, 64>(p, variant, causal, grid, s);
+    default: return fa2::launch_attn_fwd_ablate<1, 128>(p, variant, causal, grid, s);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fa2_ablate_last_error(void) { return g_err; }
+
+int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                        const int64_t q_stride[4], const int64_t k_stride[4],
+                        const int64_t v_stride[4], const int64_t o_stride[4], int32_t batch,
+                        int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                        int32_t dtype, int32_t causal, int32_t pack, float qk_scale,
+                        int32_t variant, void* stream) {
+  if (!fa2::ablation_variant_built(variant)) {
+    g_err[0] = '\0';
+    return fail(FA2_EINVAL, "variant 0x%x is not one of the built timing variants",
+                (unsigned)variant);
+  }
+  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                       n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
+                       nullptr, 0, variant, launch_ablate, stream);
+}
+
+}  // extern "C"

@@ -26,9 +26,6 @@ SIGNATURES = {
     "fa2_attn_fwd_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
                                             _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                             _i32, _i32, ctypes.c_float, _vp, _i32, _vp]),
-    "fa2_attn_fwd_variant": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64p, _i64p, _i64p, _i64p,
-                                            _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                                            ctypes.c_float, _i32, _vp]),
     "fa2_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
     "fa2_workspace_bytes_for": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                                   _i32, _i32]),
@@ -126,19 +123,6 @@ def attn_fwd_noalloc(q, k, v, out, causal, pack, block_m, block_n, qk_scale, lse
         block_m, block_n, qk_scale, None if lse is None else lse.data_ptr(), num_splits, stream)
     if rc != 0:
         raise RuntimeError(f"fa2_attn_fwd_noalloc failed ({rc}): {last_error()}")
-
-
-def attn_fwd_variant(q, k, v, out, causal, pack, qk_scale, variant, stream):
-    """Call fa2_attn_fwd_variant (the timing variants of the kernel, default tiles)."""
-    B, H_q, N_q, D = q.shape
-    H_kv, N_kv = k.shape[1], k.shape[2]
-    rc = lib().fa2_attn_fwd_variant(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-        _strides(q), _strides(k), _strides(v), _strides(out),
-        B, H_q, H_kv, N_q, N_kv, D, DTYPE_CODE[q.dtype], int(bool(causal)), pack, qk_scale,
-        variant, stream)
-    if rc != 0:
-        raise RuntimeError(f"fa2_attn_fwd_variant failed ({rc}): {last_error()}")
 
 
 def workspace_bytes(B, H_q, N_q, D, num_splits):

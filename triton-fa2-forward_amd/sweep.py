@@ -7,8 +7,10 @@ Times every (block_m, block_n) pair on one BASELINE.json workload, interleaved o
 that clock drift hits all variants alike (the reference's ablation protocol,
 bench/ablation.py:252-255), after checking each variant's output against the default one
 (max-abs within the 2e-2 bench gate). Prints one line per variant: median TFLOP/s, median ms,
-and the kernel's register, LDS and occupancy figures the library was built with are in the
-build log (hipcc -Rpass-analysis=kernel-resource-usage).
+and the compiled resources of the kernel instance that ran it, as the reference's sweep prints
+registers, spills and shared memory (bench/sweep.py:95-100): VGPRs, AGPRs, SGPRs, VGPR and SGPR
+spills, LDS per workgroup and waves per SIMD, from the compiler's own report of this build
+(fa2/kernel_resources.json, written by csrc/build.py from -Rpass-analysis=kernel-resource-usage).
 """
 
 import argparse
@@ -20,6 +22,41 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 sys.path.insert(0, os.path.dirname(HERE))
+
+
+RESOURCES_PATH = os.path.join(HERE, "fa2", "kernel_resources.json")
+
+
+def load_resources():
+    try:
+        with open(RESOURCES_PATH) as f:
+            return json.load(f)["kernels"]
+    except (OSError, KeyError, ValueError):
+        return {}
+
+
+def instance_name(dtype_code, head_dim, block_m, block_n, causal, key_table):
+    """Mangled name of the attn_fwd_kernel instance a launch with these tiles runs (the C ABI's
+    choice: block_m -> 1, 2, 4 or 8 waves of 32 rows, block_n -> 32, 64 or 128 keys; the key-norm
+    instance, VARIANT 4, only at the default configuration when the table is in use)."""
+    from fa2.kernel import _default_config
+
+    waves = 1
+    while waves * 32 < block_m:
+        waves *= 2
+    bn = 32 if block_n <= 32 else 64 if block_n <= 64 else 128
+    default_bn = _default_config(head_dim, True)[1]
+    variant = 4 if key_table and waves == 4 and bn == default_bn else 0
+    return (f"_ZN3fa215attn_fwd_kernelILi{dtype_code}ELi{head_dim}ELi{waves}ELi{bn}"
+            f"ELb{int(bool(causal))}ELi{variant}EEEvNS_6ParamsE")
+
+
+def resource_text(res):
+    if not res:
+        return "(resources: build the library to get fa2/kernel_resources.json)"
+    return (f"vgpr {res['vgprs']:3d} agpr {res['agprs']} sgpr {res['sgprs']:3d} "
+            f"spill v{res['vgpr_spills']}/s{res['sgpr_spills']} lds {res['lds_bytes'] // 1024} KiB "
+            f"{res['waves_per_simd']} waves/SIMD")
 
 
 def main():
@@ -35,6 +72,7 @@ def main():
     import torch
 
     import bench
+    from fa2 import _lib
     from fa2.kernel import attention
 
     q, k, v, causal = bench.make_inputs(args.config, "cuda")
@@ -70,16 +108,21 @@ def main():
             torch.cuda.synchronize()
             samples[(bm, bn)].append(s.elapsed_time(e) / args.iters)
         print(f"round {r + 1}/{args.rounds} done", flush=True)
+    resources = load_resources()
+    key_table = (_lib.workspace_bytes_for(B, H_q, k.shape[1], N, k.shape[2], D, q.dtype, causal, 1)
+                 > _lib.workspace_bytes(B, H_q, N, D, 1))
     rows = []
     for (bm, bn), ms in samples.items():
         med = statistics.median(ms)
+        name = instance_name(_lib.DTYPE_CODE[q.dtype], D, bm, bn, causal, key_table)
         rows.append({"block_m": bm, "block_n": bn, "median_ms": med,
-                     "tflops": flops / (med * 1e-3) / 1e12, "samples_ms": ms})
+                     "tflops": flops / (med * 1e-3) / 1e12, "samples_ms": ms,
+                     "kernel": name, "resources": resources.get(name)})
     rows.sort(key=lambda r: r["median_ms"])
     print(f"{bench.describe(args.config)}: median over {args.rounds} interleaved rounds of {args.iters}")
     for r in rows:
         print(f"  block_m={r['block_m']:4d} block_n={r['block_n']:4d}  {r['median_ms']:8.4f} ms  "
-              f"{r['tflops']:7.1f} TFLOP/s", flush=True)
+              f"{r['tflops']:7.1f} TFLOP/s  {resource_text(r['resources'])}", flush=True)
     if args.json:
         with open(args.json, "w") as f:
             json.dump({"config": args.config, "rows": rows}, f, indent=1)
