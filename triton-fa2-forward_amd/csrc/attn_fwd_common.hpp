@@ -214,11 +214,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the XCDs round-robin; block b runs on XCD b % 8.
 //   * When the (batch, kv head) units split evenly over the XCDs, each XCD owns a fixed set of
 //     whole units, so its L2 holds the K/V of the heads it works on (C3: HBM reads fell from
-//     635 to 139 MiB per launch). Inside an XCD the order is q tile outermost (heaviest causal
+//     635 to 139 MiB per launch). Causal: inside an XCD the order is q tile outermost (heaviest
 //     tile first) across all of its units, then unit, then the query-head groups sharing a KV
 //     head. Unit after unit instead started the last unit's heaviest tiles late and left the
 //     XCD's slots 22% idle on C2 (8 units per XCD): the q-tile-major order runs C2 12% faster,
 //     although its L2 now misses more (reads past L2 192 -> ~680 MiB per launch, ~2.6 TB/s).
+//     Non-causal programs all do the same work, so there the order is unit after unit: the
+//     programs in flight on an XCD then share one unit's K/V in its L2 (C4: four units per XCD
+//     read K/V 8.3x over in q-tile-major order).
 //   * Otherwise a fixed unit set per XCD would hand one XCD more of the heavy causal tiles than
 //     another (C5, 12 units over 8 XCDs: 15% more work on XCD 0). Then the order is q tile
 //     outermost over all units, heaviest first, and the round-robin dealing balances the XCDs.
@@ -241,11 +244,22 @@ __device__ __forceinline__ Program program_of(const Params& p, int block) {
   if (units % kXcds == 0) {
     const int xcd = block % kXcds, slot = block / kXcds;
     const int upx = units / kXcds;             // units per XCD
-    const int per_t = upx * progs_per_kv;      // programs per q tile on one XCD
-    t = slot / per_t;
-    const int r = slot - t * per_t;
-    kv_index = xcd * upx + r / progs_per_kv;   // b * h_kv + hkv
-    h_in = r % progs_per_kv;
+    if (CAUSAL) {
+      const int per_t = upx * progs_per_kv;    // programs per q tile on one XCD
+      t = slot / per_t;
+      const int r = slot - t * per_t;
+      kv_index = xcd * upx + r / progs_per_kv; // b * h_kv + hkv
+      h_in = r % progs_per_kv;
+    } else {
+      // every program has the same work: unit after unit, so that the XCD's programs in flight
+      // stream one unit's K/V through its L2 instead of several units' at once
+      const int per_u = p.n_tiles * progs_per_kv;  // programs of one unit
+      const int u = slot / per_u;
+      const int r = slot - u * per_u;
+      t = r / progs_per_kv;
+      h_in = r - t * progs_per_kv;
+      kv_index = xcd * upx + u;
+    }
   } else {
     const int grid = p.n_tiles * p.n_bh;
     if (CAUSAL && grid <= 3 * kCus && block >= kCus) {
