@@ -29,8 +29,15 @@ Protocol (the reference's, bench/bench.py:51-92, restated for ROCm):
   * cpu_baseline: the oracle's blocked_attention (the reference's CPU path, fa2/reference.py:
     35-82, restated) timed on this host, one thread, on whole (batch, head) pairs of the
     workload until at least 10 s of CPU work, reported as its TFLOP/s;
-  * roofline.traffic: HBM bytes per launch from the committed rocprofv3 counter summary
-    (profiles/hbm_traffic.json), next to the algorithmic minimum (q, k, v read, out written).
+  * roofline.traffic: bytes per launch that left L2 (TCC FETCH_SIZE + WRITE_SIZE, copy-calibrated;
+    Infinity Cache hits count too, so DRAM traffic is at most this) from the committed rocprofv3
+    summary (profiles/l2_miss_traffic.json), next to the algorithmic minimum (q, k, v read, out
+    written);
+  * clock: the graphics clock (mean over the XCDs) and socket power sampled with amdsmi during
+    the timed steps and during 1 s of sustained steps; roofline.frac_at_sampled_sclk divides by
+    the dense peak at that clock instead of at 2.4 GHz;
+  * value_reference_protocol: the reference's own protocol (flush, events per launch, median)
+    beside `value`;
 
 Prints ONE JSON line. --gpus N with N > 1 exits: this build is one GPU per box.
 """
@@ -264,29 +271,174 @@ def cpu_baseline(name, q, k, v, causal, min_seconds=10.0):
 
 
 def measured_traffic(name):
-    """HBM bytes per launch for this workload from the committed rocprofv3 counter summary
-    (profiles/hbm_traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what
-    the counter reads for a plain copy of known size), or None."""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    """Bytes per launch that left L2 for this workload, from the committed rocprofv3 counter
+    summary (profiles/l2_miss_traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by
+    what the counter reads for a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "l2_miss_traffic.json")
     try:
         with open(path) as f:
             entry = json.load(f)["configs"][name]
-        return {"bytes": entry["bytes"], "source": f"profiles/hbm_traffic.json ({entry['kernel_build']})"}
+        return {"bytes": entry["bytes"], "source": f"profiles/l2_miss_traffic.json ({entry['kernel_build']})"}
     except (OSError, KeyError, ValueError):
         return None
 
 
+def _read(path):
+    try:
+        with open(path) as f:
+            return f.read().strip()
+    except OSError:
+        return None
+
+
+def _sha256(path):
+    import hashlib
+
+    try:
+        with open(path, "rb") as f:
+            return hashlib.sha256(f.read()).hexdigest()
+    except OSError:
+        return None
+
+
+def _hipcc_version():
+    import shutil
+    import subprocess
+
+    cc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    try:
+        out = subprocess.run([cc, "--version"], capture_output=True, text=True, timeout=30).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    lines = [l.strip() for l in out.splitlines() if l.strip()]
+    return " | ".join(lines[:2]) or None
+
+
 def gpu_env():
+    """The run environment (the reference records driver, versions and date with every result,
+    bench/bench.py:196-219): GPU, ROCm, HIP, hipcc, torch, Python, the driver as amdsmi reports
+    it, the SHA-256 of the library that ran, and the UTC date."""
+    import datetime
+    import platform
+
     import torch
 
+    from fa2 import _lib
+
     props = torch.cuda.get_device_properties(0)
-    return {
+    env = {
         "gpu": props.name or getattr(props, "gcnArchName", ""),
         "arch": getattr(props, "gcnArchName", None),
         "cus": props.multi_processor_count,
+        "rocm": _read("/opt/rocm/.info/version"),
+        "hip_runtime": torch.version.hip,
+        "hipcc": _hipcc_version(),
         "torch": torch.__version__,
-        "hip": torch.version.hip,
+        "python": platform.python_version(),
+        "kernel": platform.release(),
+        "library": _lib.LIB_PATH.replace(ROOT + os.sep, ""),
+        "library_sha256": _sha256(_lib.LIB_PATH),
+        "date_utc": datetime.datetime.now(datetime.timezone.utc).isoformat(timespec="seconds"),
+        "host_cpus": os.cpu_count(),
     }
+    try:
+        import amdsmi
+
+        amdsmi.amdsmi_init()
+        try:
+            h = amdsmi.amdsmi_get_processor_handles()[0]
+            drv = amdsmi.amdsmi_get_gpu_driver_info(h)
+            env["driver"] = f"{drv.get('driver_name')} {drv.get('driver_version')}"
+            clk = amdsmi.amdsmi_get_clock_info(h, amdsmi.AmdSmiClkType.GFX)
+            env["sclk_range_mhz"] = [clk.get("min_clk"), clk.get("max_clk")]
+            pw = amdsmi.amdsmi_get_power_info(h)
+            env["power_limit_w"] = (pw.get("power_limit") / 1e6 if isinstance(pw.get("power_limit"), (int, float))
+                                    else pw.get("power_limit"))
+        finally:
+            amdsmi.amdsmi_shut_down()
+    except Exception as e:  # noqa: BLE001 - the environment record is best effort
+        env["driver"] = f"unavailable ({type(e).__name__})"
+    return env
+
+
+class ClockSampler:
+    """Samples the GPU's graphics clock (every XCD's, MHz) and socket power (W) with amdsmi on a
+    background thread while GPU work runs (the reference samples clock and power beside its runs,
+    bench/results/2026-10-03/clock.py:7-8). One amdsmi call takes ~0.3 ms; the thread sleeps
+    `period_s` between calls and takes no GIL while it sleeps, so the launches it runs beside
+    are not held up. Device 0 is the only GPU of the box."""
+
+    def __init__(self, period_s=0.002):
+        self.period_s = period_s
+        self.sclk, self.power, self.error = [], [], None
+        self._stop = None
+        self._thread = None
+
+    def __enter__(self):
+        import threading
+
+        self._stop = threading.Event()
+        try:
+            import amdsmi
+
+            amdsmi.amdsmi_init()
+            self._amdsmi = amdsmi
+            self._h = amdsmi.amdsmi_get_processor_handles()[0]
+        except Exception as e:  # noqa: BLE001
+            self.error = f"amdsmi unavailable: {type(e).__name__}: {e}"
+            return self
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self._thread.start()
+        return self
+
+    def _run(self):
+        while not self._stop.is_set():
+            try:
+                m = self._amdsmi.amdsmi_get_gpu_metrics_info(self._h)
+                clks = [c for c in m.get("current_gfxclks", []) if isinstance(c, (int, float))]
+                if clks:
+                    self.sclk.append(sum(clks) / len(clks))
+                pw = m.get("current_socket_power")
+                if isinstance(pw, (int, float)):
+                    self.power.append(float(pw))
+            except Exception as e:  # noqa: BLE001
+                self.error = f"{type(e).__name__}: {e}"
+                return
+            self._stop.wait(self.period_s)
+
+    def __exit__(self, *exc):
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+            self._amdsmi.amdsmi_shut_down()
+        return False
+
+    def summary(self):
+        if not self.sclk:
+            return {"samples": 0, "error": self.error or "no samples"}
+        return {"samples": len(self.sclk),
+                "sclk_mhz_median": round(statistics.median(self.sclk), 1),
+                "sclk_mhz_min": round(min(self.sclk), 1), "sclk_mhz_max": round(max(self.sclk), 1),
+                "power_w_median": round(statistics.median(self.power), 1) if self.power else None,
+                "power_w_max": round(max(self.power), 1) if self.power else None}
+
+
+def sustained_clock(fn, seconds=1.0):
+    """Steps back to back for `seconds` with the clock sampler running: the clock and power the
+    kernel sustains (the timed steps of a short kernel last only a few milliseconds)."""
+    import torch
+
+    with ClockSampler() as smp:
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(10):
+                fn()
+            n += 10
+            torch.cuda.synchronize()
+    out = smp.summary()
+    out["steps"] = n
+    return out
 
 
 def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
@@ -314,17 +466,31 @@ def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
     kernels = (["fa2::key_norm_kernel"] if key_norm else []) + ["fa2::attn_fwd_kernel"]
 
     settle = settle_clocks(fn)
-    total_ms, wall_ms = time_steps(fn, steps, warmup)
+    with ClockSampler() as timed_clock:
+        total_ms, wall_ms = time_steps(fn, steps, warmup)
     avg_kernel_ms = total_ms / steps   # one step: the kernels above, back to back
+    clock = {"timed_steps": timed_clock.summary(), "sustained_1s": sustained_clock(fn)}
     per = time_each(fn, steps)
     q1, med, q3 = statistics.quantiles(per, n=4, method="inclusive") if len(per) > 1 else (per[0],) * 3
     value = flops * steps / (total_ms * 1e-3) / 1e12
     achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
     traffic = measured_traffic(name)
     min_bytes = sum(t.numel() * t.element_size() for t in (q, k, v)) + out.numel() * out.element_size()
+    fl = None
+    if flush_iters:
+        fl = flushed_median(fn, flush_iters)
+        fl["tflops"] = round(flops / (fl["median_ms"] * 1e-3) / 1e12, 2)
+    # the dense peak at the clock the kernel ran at: CUs x sampled sclk x 4096 FLOP/clk
+    sclk = clock["timed_steps"].get("sclk_mhz_median") or clock["sustained_1s"].get("sclk_mhz_median")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    peak_at_sclk = cus * sclk * 1e6 * 4096 / 1e12 if sclk else None
     res = {
         "metric": METRIC,
         "value": round(value, 2),
+        "value_reference_protocol": {
+            "tflops": fl["tflops"] if fl else None,
+            "protocol": "the reference's (bench/bench.py:61-80): 1 GiB flush before every launch, "
+                        "HIP events around each launch, median"},
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": steps,
@@ -343,9 +509,15 @@ def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(PEAK_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_counts": "L2-miss bytes: TCC FETCH_SIZE + WRITE_SIZE, the requests that "
+                                       "left L2 (Infinity Cache hits included, so DRAM bytes are at most "
+                                       "this), copy-calibrated",
                      "traffic_source": traffic["source"] if traffic else None,
                      "algorithmic_bytes": min_bytes,
-                     "kernel": " + ".join(kernels), "avg_kernel_ms": round(avg_kernel_ms, 5)},
+                     "kernel": " + ".join(kernels), "avg_kernel_ms": round(avg_kernel_ms, 5),
+                     "peak_at_sampled_sclk": round(peak_at_sclk, 1) if peak_at_sclk else None,
+                     "frac_at_sampled_sclk": round(achieved / peak_at_sclk, 4) if peak_at_sclk else None},
+        "clock": clock,
         "per_launch_events": {"median_ms": round(med, 5), "p25_ms": round(q1, 5), "p75_ms": round(q3, 5),
                               "slowest_steps": [[i, round(per[i], 4)] for i in
                                                 sorted(range(len(per)), key=per.__getitem__)[-3:]]},
@@ -355,9 +527,7 @@ def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
         "env": gpu_env(),
         "library": _lib.lib().fa2_version().decode(),
     }
-    if flush_iters:
-        fl = flushed_median(fn, flush_iters)
-        fl["tflops"] = round(flops / (fl["median_ms"] * 1e-3) / 1e12, 2)
+    if fl:
         res["flushed"] = fl
     if with_sdpa:
         res["sdpa_same_box"] = sdpa_rate(q, k, v, causal, flops)

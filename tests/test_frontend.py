@@ -426,3 +426,38 @@ def test_build_records_the_resources_of_every_product_instance():
                         assert r["vgprs"] > 0 and r["lds_bytes"] > 0 and r["waves_per_simd"] >= 1
                 r = res[sweep.instance_name(dt, d, 128, 0 or _default_config(d, True)[1], causal, True)]
                 assert r["variant"] == 4
+
+
+@needs_lib
+def test_fa2_installs_as_a_package(tmp_path):
+    """`pip install .` puts the drop-in under its reference import name with the built library
+    inside, so `from fa2.kernel import
+    attention` works without PYTHONPATH edits (setup.cfg maps fa2 to triton-fa2-forward_amd/fa2).
+    Installed into a scratch target from a copy of the
+    project files (no network: the build backend is the installed setuptools)."""
+    import shutil
+    import subprocess
+    import sys
+
+    src = tmp_path / "src"
+    (src / "triton-fa2-forward_amd").mkdir(parents=True)
+    shutil.copy(os.path.join(ROOT, "pyproject.toml"), src)
+    shutil.copy(os.path.join(ROOT, "setup.cfg"), src)
+    shutil.copytree(os.path.join(ROOT, "triton-fa2-forward_amd", "fa2"),
+                    src / "triton-fa2-forward_amd" / "fa2",
+                    ignore=shutil.ignore_patterns("__pycache__"))
+    target = tmp_path / "site"
+    res = subprocess.run([sys.executable, "-m", "pip", "install", "--no-build-isolation", "--no-deps",
+                          "--no-index", "--quiet", "--target", str(target), str(src)],
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert (target / "fa2" / "libfa2_fwd.so").exists()
+    probe = ("import fa2.kernel, fa2._lib as L; print(fa2.kernel.__file__); "
+             "print(L.lib().fa2_version().decode())")
+    env = {k: v for k, v in os.environ.items() if k != "PYTHONPATH"}
+    env["PYTHONPATH"] = str(target)
+    res = subprocess.run([sys.executable, "-c", probe], capture_output=True, text=True, timeout=300,
+                         cwd=str(tmp_path), env=env)
+    assert res.returncode == 0, res.stdout + res.stderr
+    kernel_file, version = res.stdout.split("\n")[:2]
+    assert kernel_file.startswith(str(target)) and "gfx950" in version
