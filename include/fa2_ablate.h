@@ -59,6 +59,29 @@ FA2_API int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, voi
                                 int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,
                                 int32_t pack, float qk_scale, int32_t variant, void* stream);
 
+/* Words per workgroup that fa2_ablate_timeline records. */
+#define FA2_ABLATE_TIMELINE_WORDS 6
+
+/*
+ * fa2_ablate_timeline - the product kernel (variant 0, same output bit for bit) with a timeline:
+ * every workgroup b writes FA2_ABLATE_TIMELINE_WORDS uint64 at records[6 b ...]:
+ *   [0] entry, [1] prologue done (Q and the first K/V tiles in, first barrier passed),
+ *   [2] tile loop done, [3] stores done (after a wait for them): s_memrealtime, 100 MHz;
+ *   [4] the workgroup's K/V tile count;
+ *   [5] XCC_ID << 32 | HW_ID (hardware ids of the wave that wrote: CU, shader array, engine).
+ * It waits for its stores before the last stamp, which the product does not do. No counterpart
+ * in the reference (its profiling used Nsight); a measurement tool for the schedule of short
+ * grids. records: device memory, 8-byte aligned, at least 6 x workgroups words (record_words),
+ * where workgroups = ceil(n_q * pack / 128) * batch * h_q / pack; else FA2_EINVAL, no launch.
+ */
+FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
+                                const int64_t q_stride[4], const int64_t k_stride[4],
+                                const int64_t v_stride[4], const int64_t o_stride[4],
+                                int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                                int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,
+                                int32_t pack, float qk_scale, uint64_t* records,
+                                int64_t record_words, void* stream);
+
 /* Thread-local description of this library's last failure in this thread ("" if none). */
 FA2_API const char* fa2_ablate_last_error(void);
 

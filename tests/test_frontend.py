@@ -334,11 +334,11 @@ def test_product_library_exports_its_api_and_no_timing_variant():
 def test_measurement_library_exports_exactly_its_header():
     names = _exported(ABLATE_LIB)
     assert {n for n in names if n.startswith("fa2_")} == _c_names(ABLATE_HEADER) == {
-        "fa2_ablate_attn_fwd", "fa2_ablate_last_error"}
+        "fa2_ablate_attn_fwd", "fa2_ablate_timeline", "fa2_ablate_last_error"}
     # the knockouts are compiled into it: kernel instances with the no_exp, no_softmax and
-    # kv_l2 bits, and matmul_only (no_softmax | kv_l2)
+    # kv_l2 bits, and matmul_only (no_softmax | kv_l2); and the timeline instance (64)
     variants = {int(m.group(1)) for n in names for m in [re.search(r"ELb[01]ELi(\d+)EEEv", n)] if m}
-    assert variants == {0, 1, 2, 3, 8, 16, 32, 48}
+    assert variants == {0, 1, 2, 3, 8, 16, 32, 48, 64}
 
 
 @needs_ablate
@@ -348,7 +348,9 @@ def test_measurement_library_rejects_unbuilt_variants_before_any_launch():
     arr = lambda s: (ctypes.c_int64 * 4)(*s)  # noqa: E731
     lib = ablate_lib()
     st = arr((8192, 2048, 64, 1))
-    for bad in (4, 5, 24, 64, -1):      # 4: the key-norm instance is the product's, not a variant
+    # 4: the key-norm instance is the product's, not a variant; 64: the timeline instance runs
+    # only through fa2_ablate_timeline, which checks its record buffer
+    for bad in (4, 5, 24, 64, 65, -1):
         rc = lib.fa2_ablate_attn_fwd(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
                                      32, 64, 0, 1, 1, 0.18, bad, None)
         assert rc == -1 and b"variant" in lib.fa2_ablate_last_error(), (bad, rc)
@@ -356,6 +358,27 @@ def test_measurement_library_rejects_unbuilt_variants_before_any_launch():
     rc = lib.fa2_ablate_attn_fwd(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
                                  32, 48, 0, 1, 1, 0.18, 8, None)
     assert rc == -1 and b"head_dim" in lib.fa2_ablate_last_error()
+
+
+@needs_ablate
+def test_timeline_needs_a_buffer_of_six_words_per_workgroup():
+    """fa2_ablate_timeline rejects a missing, misaligned or short record buffer before any
+    launch (fake device pointers): B 1, H 4, N 32 -> 4 workgroups -> 24 words."""
+    from ablation import ablate_lib
+
+    arr = lambda s: (ctypes.c_int64 * 4)(*s)  # noqa: E731
+    lib = ablate_lib()
+    fn = lib.fa2_ablate_timeline
+    fn.restype = ctypes.c_int
+    i32, i64p, vp = ctypes.c_int32, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p
+    fn.argtypes = [vp, vp, vp, vp, i64p, i64p, i64p, i64p] + [i32] * 9 + \
+        [ctypes.c_float, vp, ctypes.c_int64, vp]
+    st = arr((8192, 2048, 64, 1))
+    for rec, words, code, msg in ((None, 24, -1, b"null"), (0x10004, 24, -2, b"aligned"),
+                                  (0x10000, 23, -1, b"24 words")):
+        rc = fn(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32, 32, 64, 0, 1, 1,
+                0.18, rec, words, None)
+        assert rc == code and msg in lib.fa2_ablate_last_error(), (rc, lib.fa2_ablate_last_error())
 
 
 def test_ablation_front_end_checks_arguments_on_the_cpu():

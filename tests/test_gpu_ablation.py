@@ -98,3 +98,26 @@ def test_knockouts_change_the_output(knobs, causal, dtype, D):
     q, k, v = make_qkv(BATCH, 4, 2, 300, 300, D, dtype)
     out = _ablate()(q, k, v, causal=causal, **knobs)
     assert not torch.equal(out, attention(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("dtype,D,causal", [(torch.bfloat16, 128, True), (torch.float16, 64, False)])
+def test_timeline_instance_is_the_product_and_its_records_are_ordered(dtype, D, causal):
+    """fa2_ablate_timeline (triton-fa2-forward_amd/timeline.py): the product's output bit for bit,
+    and every workgroup's stamps in order (entry <= prologue <= loop <= stores done), its tile
+    count that of its program (causal: 2 t + 2 tiles of 64 keys for q tile t, capped at the
+    sequence), and hardware ids that name at most 256 CUs."""
+    from ablation import table_free_launch
+    from timeline import decode_cu, run_timeline
+
+    N = 1000
+    q, k, v = make_qkv(2, 8, 2, N, N, D, dtype)
+    recs, out = run_timeline(q, k, v, causal, 2)
+    assert torch.equal(out, table_free_launch(q, k, v, causal))
+    n_tiles_kv = -(-N // 64)
+    tiles_seen = sorted(r[4] for r in recs)
+    want = sorted(min(2 * t + 2, n_tiles_kv) if causal else n_tiles_kv
+                  for t in range(-(-N // 128)) for _ in range(2 * 8))
+    assert tiles_seen == want
+    for e, p, l, d, tiles, hw in recs:
+        assert 0 < e <= p <= l <= d and d - e < 10**6   # under 10 ms
+    assert len({decode_cu(r[5]) for r in recs}) <= 256

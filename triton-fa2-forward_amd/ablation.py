@@ -185,7 +185,11 @@ def measure_shape(args, N):
     shipped = attention(q, k, v, causal=causal)
     launchers = {"attention()": lambda: attention(q, k, v, causal=causal)}
     outputs = {}
+    group = args.hq // args.hkv
     for name in args.variants:
+        if name == "pack" and (group == 1 or 128 % group):
+            print(f"(pack skipped: GQA group {group} does not pack into 128-row programs)")
+            continue
         launchers[name] = launcher(name, q, k, v, causal)
         outputs[name] = launchers[name]()
     torch.cuda.synchronize()

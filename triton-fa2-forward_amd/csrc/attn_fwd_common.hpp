@@ -55,6 +55,13 @@ constexpr int kVariantKeyBound = 4;
 constexpr int kVariantNoExp = 8;       // exp2 replaced by its argument (alpha too)
 constexpr int kVariantNoSoftmax = 16;  // no mask, row max, exp, sum or rescale: O = (Q K^T) V
 constexpr int kVariantKvL2 = 32;       // every tile loads the first K/V tile again (L2 hits)
+// Measurement library only, and computes the product's attention: every workgroup also records
+// its timeline (Params::timeline, kTimelineWords words); waits for its stores before the last stamp.
+constexpr int kVariantTimeline = 64;
+// s_getreg operands (register id | offset << 6 | (size - 1) << 11) of the whole 32-bit HW_ID
+// register (id 4: wave, SIMD, CU, shader array and engine of the wave) and XCC_ID (id 20).
+constexpr int kHwregHwId = 4 | (31 << 11);
+constexpr int kHwregXccId = 20 | (31 << 11);
 
 // ---------------------------------------------------------------------------------
 // element type traits: the MFMA, the fp32 -> 16-bit pair conversion (RNE) and the fp32 sum of

@@ -111,7 +111,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
                   int32_t dtype, int32_t causal, int32_t pack, int32_t block_m, int32_t block_n,
                   float qk_scale, float* lse, int32_t num_splits, void* workspace,
                   size_t workspace_bytes, int32_t variant, KernelLaunch launch_kernel,
-                  void* stream) {
+                  void* stream, uint64_t* timeline = nullptr, int64_t timeline_words = 0) {
   g_err[0] = '\0';
   // ---- shape checks (fa2/kernel.py:218-228)
   if (batch < 0 || h_q <= 0 || h_kv <= 0 || n_q < 0 || n_kv < 0)
@@ -219,6 +219,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   p.split_tiles = 0;
   p.key_norm2 = nullptr;
   p.key_chunks = 0;
+  p.timeline = nullptr;
 
   // Split-KV: cut the key range into whole tiles; drop splits that would be empty.
   const int64_t kv_tiles = ((int64_t)n_kv + bn - 1) / bn;
@@ -247,6 +248,13 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   const int64_t grid = n_tiles * n_bh * splits;
   if (grid > 0x7fffffffLL)
     return fail(FA2_EINVAL, "grid of %lld workgroups is too large", (long long)grid);
+  if (timeline) {  // the measurement library's timeline variant: kTimelineWords per workgroup
+    if (timeline_words < grid * fa2::kTimelineWords)
+      return fail(FA2_EINVAL, "the timeline needs %lld words for %lld workgroups, got %lld",
+                  (long long)(grid * fa2::kTimelineWords), (long long)grid,
+                  (long long)timeline_words);
+    p.timeline = timeline;
+  }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   // Key-norm table: used whenever the workspace has room for it beyond the split-KV partials of

@@ -69,6 +69,9 @@ void attn_fwd_kernel(const Params p) {
   constexpr bool kNoExp = (VARIANT & kVariantNoExp) != 0;
   constexpr bool kNoSoftmax = (VARIANT & kVariantNoSoftmax) != 0;
   constexpr bool kKvL2 = (VARIANT & kVariantKvL2) != 0;
+  constexpr bool kTimeline = (VARIANT & kVariantTimeline) != 0;
+  const uint64_t tl_entry = kTimeline ? __builtin_amdgcn_s_memrealtime() : 0;
+  uint64_t tl_prologue = 0, tl_loop = 0;
   // exp2, or (knockout) its argument
   auto ex2 = [](float x) { return kNoExp ? x : __builtin_amdgcn_exp2f(x); };
   constexpr int KS = D / 16;               // 16-dim k-steps of S^T = K Q^T
@@ -317,6 +320,7 @@ void attn_fwd_kernel(const Params p) {
         wait_vmcnt<0>();
       }
       __syncthreads();
+      if constexpr (kTimeline) tl_prologue = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
       for (int ks = 0; ks < LA_S; ++ks)
 #pragma unroll
@@ -660,6 +664,7 @@ void attn_fwd_kernel(const Params p) {
         wait_vmcnt<0>();
       }
       __syncthreads();
+      if constexpr (kTimeline) tl_prologue = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
       for (int ks = 0; ks < LA; ++ks)
 #pragma unroll
@@ -707,6 +712,8 @@ void attn_fwd_kernel(const Params p) {
       pv_product(pb, bufv, va);
     }
   }
+
+  if constexpr (kTimeline) tl_loop = __builtin_amdgcn_s_memrealtime();
 
   // ---- normalise once, store once (fa2/kernel.py:178-183)
   // (knockout without softmax: l = 1, as the reference's l_i + 1 on a zero sum)
@@ -761,6 +768,23 @@ void attn_fwd_kernel(const Params p) {
           }
         }
       if (p.lse && g == 0) p.lse[row_index] = lse2_exact * kLn2;
+    }
+  }
+
+  // ---- timeline variant (measurement library): the workgroup's stamps, once every wave's
+  // stores have completed. Written by one lane with an ordinary vector store.
+  if constexpr (kTimeline) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t* rec = p.timeline + (int64_t)blockIdx.x * kTimelineWords;
+      rec[0] = tl_entry;
+      rec[1] = tl_prologue;
+      rec[2] = tl_loop;
+      rec[3] = __builtin_amdgcn_s_memrealtime();
+      rec[4] = (uint64_t)n_tiles_kv;
+      rec[5] = ((uint64_t)__builtin_amdgcn_s_getreg(kHwregXccId) << 32) |
+               (uint64_t)__builtin_amdgcn_s_getreg(kHwregHwId);
     }
   }
 }

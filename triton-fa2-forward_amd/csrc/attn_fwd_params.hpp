@@ -46,7 +46,15 @@ struct Params {
   // more than kBoundTau (Cauchy-Schwarz) and then skips the per-tile row max.
   const float* key_norm2;  // [B * H_kv][key_chunks]
   int32_t key_chunks;      // ceil(n_kv / kKeyChunk)
+  // Measurement library only (the timeline variant): kTimelineWords uint64 per workgroup,
+  // indexed by blockIdx.x. Null, and never read, in the product's instances.
+  uint64_t* timeline;
 };
+
+// Words per workgroup of the timeline variant: entry, prologue done (first barrier), tile loop
+// done, stores done (s_memrealtime, 100 MHz), the workgroup's K/V tile count, and its hardware
+// ids (XCC_ID << 32 | HW_ID).
+constexpr int kTimelineWords = 6;
 
 // Arguments of the key-norm pass (attn_key_norm.hip).
 struct KeyNormParams {

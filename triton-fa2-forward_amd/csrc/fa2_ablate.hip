@@ -37,7 +37,8 @@ int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
                         int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
                         int32_t dtype, int32_t causal, int32_t pack, float qk_scale,
                         int32_t variant, void* stream) {
-  if (!fa2::ablation_variant_built(variant)) {
+  // the timeline instance writes its records: only fa2_ablate_timeline, with a buffer, runs it
+  if (!fa2::ablation_variant_built(variant) || (variant & fa2::kVariantTimeline)) {
     g_err[0] = '\0';
     return fail(FA2_EINVAL, "variant 0x%x is not one of the built timing variants",
                 (unsigned)variant);
@@ -45,6 +46,22 @@ int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
   return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
                        n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
                        nullptr, 0, variant, launch_ablate, stream);
+}
+
+int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
+                        const int64_t q_stride[4], const int64_t k_stride[4],
+                        const int64_t v_stride[4], const int64_t o_stride[4], int32_t batch,
+                        int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                        int32_t dtype, int32_t causal, int32_t pack, float qk_scale,
+                        uint64_t* records, int64_t record_words, void* stream) {
+  g_err[0] = '\0';
+  if (!records) return fail(FA2_EINVAL, "null timeline buffer");
+  if (reinterpret_cast<uintptr_t>(records) & 7u)
+    return fail(FA2_EALIGN, "the timeline buffer must be 8-byte aligned");
+  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                       n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
+                       nullptr, 0, fa2::kVariantTimeline, launch_ablate, stream, records,
+                       record_words);
 }
 
 }  // extern "C"
