@@ -371,6 +371,7 @@ class ClockSampler:
     def __init__(self, period_s=0.002):
         self.period_s = period_s
         self.sclk, self.power, self.error = [], [], None
+        self.per_xcd = []
         self._stop = None
         self._thread = None
 
@@ -398,6 +399,7 @@ class ClockSampler:
                 clks = [c for c in m.get("current_gfxclks", []) if isinstance(c, (int, float))]
                 if clks:
                     self.sclk.append(sum(clks) / len(clks))
+                    self.per_xcd.append(clks)
                 pw = m.get("current_socket_power")
                 if isinstance(pw, (int, float)):
                     self.power.append(float(pw))
@@ -420,7 +422,9 @@ class ClockSampler:
                 "sclk_mhz_median": round(statistics.median(self.sclk), 1),
                 "sclk_mhz_min": round(min(self.sclk), 1), "sclk_mhz_max": round(max(self.sclk), 1),
                 "power_w_median": round(statistics.median(self.power), 1) if self.power else None,
-                "power_w_max": round(max(self.power), 1) if self.power else None}
+                "power_w_max": round(max(self.power), 1) if self.power else None,
+                "sclk_mhz_median_per_xcd": [round(statistics.median(c), 1) for c in zip(*self.per_xcd)]
+                if self.per_xcd else None}
 
 
 def sustained_clock(fn, seconds=1.0):
