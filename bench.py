@@ -445,7 +445,23 @@ def sustained_clock(fn, seconds=1.0):
     return out
 
 
-def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
+def measured_ceiling(seconds=1.0):
+    """The MFMA rate this box sustains under its power limit (triton-fa2-forward_amd/ceiling.py,
+    fa2_ablate_mfma_ceiling in the measurement library): bf16 MFMAs on random operands alone, and
+    with the attention kernel's LDS operand reads and softmax vector work beside them. The nominal
+    peak assumes 2.4 GHz; on random data the chip holds its power by running lower."""
+    try:
+        import ceiling
+
+        out = {m: ceiling.measure(m, seconds) for m in ("mfma", "mfma_lds_softmax")}
+    except Exception as e:  # noqa: BLE001
+        return {"error": f"{type(e).__name__}: {e}"}
+    out["source"] = ("fa2_ablate_mfma_ceiling (libfa2_ablate.so, csrc/mfma_ceiling.hip), "
+                     f"each mode alone for {seconds:g} s in this run")
+    return out
+
+
+def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False, ceiling=None):
     import torch
 
     from fa2 import _lib
@@ -531,6 +547,12 @@ def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False):
         "env": gpu_env(),
         "library": _lib.lib().fa2_version().decode(),
     }
+    if ceiling is not None:
+        res["roofline"]["measured_ceiling"] = ceiling
+        top = ceiling.get("mfma", {}).get("tflops")
+        mix = ceiling.get("mfma_lds_softmax", {}).get("tflops")
+        res["roofline"]["frac_of_measured_mfma_ceiling"] = round(achieved / top, 4) if top else None
+        res["roofline"]["frac_of_measured_mix_ceiling"] = round(achieved / mix, 4) if mix else None
     if fl:
         res["flushed"] = fl
     if with_sdpa:
@@ -607,6 +629,8 @@ def main():
     ap.add_argument("--pack-short", action="store_true",
                     help="instead of C3: the reference's few-queries table, one line per N_q")
     ap.add_argument("--flush-iters", type=int, default=10, help="iterations of the flushed pass (0: skip)")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="skip the measured MFMA ceiling (fa2_ablate_mfma_ceiling, ~3 s)")
     ap.add_argument("--sdpa", action="store_true",
                     help="also time torch's fused SDPA on the same inputs (sdpa_same_box, context)")
     args = ap.parse_args()
@@ -627,9 +651,10 @@ def main():
             print(json.dumps(run_pack_short(n_q, args.steps, args.warmup)), flush=True)
         return
     names = ["C3", "C2", "C4", "C5"] if args.all else [args.config]
+    ceil = None if args.no_ceiling else measured_ceiling()
     for i, name in enumerate(names):
         res = run(name, args.steps, args.warmup, with_cpu=(i == 0 and not args.no_cpu_baseline),
-                  flush_iters=args.flush_iters, with_sdpa=args.sdpa)
+                  flush_iters=args.flush_iters, with_sdpa=args.sdpa, ceiling=ceil)
         print(json.dumps(res), flush=True)
 
 

@@ -82,6 +82,29 @@ FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, voi
                                 int32_t pack, float qk_scale, uint64_t* records,
                                 int64_t record_words, void* stream);
 
+/* Modes of fa2_ablate_mfma_ceiling. */
+#define FA2_ABLATE_CEIL_MFMA 0              /* random bf16 operands in registers            */
+#define FA2_ABLATE_CEIL_MFMA_CONST 1        /* the same with constant operands (1.0)        */
+#define FA2_ABLATE_CEIL_MFMA_LDS 2          /* random, one 1 KiB ds_read_b128 per MFMA      */
+#define FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX 3  /* that plus the softmax's vector work per MFMA */
+#define FA2_ABLATE_CEIL_MAX_WORKGROUPS 65536
+#define FA2_ABLATE_CEIL_MAX_ITERS 100000
+
+/*
+ * fa2_ablate_mfma_ceiling - what the matrix cores sustain on this chip with the attention
+ * kernel's launch shape (256-thread workgroups, 64 KiB LDS each: two per CU): every wave issues
+ * iters x 16 v_mfma_f32_32x32x16_bf16 (32768 FLOP each) on two independent accumulators, with
+ * the per-MFMA extra work of `mode` (FA2_ABLATE_CEIL_*) on independent data. One launch does
+ * workgroups x 4 x iters x 16 x 32768 FLOP. The chip lowers its clock to hold its power limit,
+ * and an MFMA's energy depends on its operands, so the rate depends on the mode and on how long
+ * it runs; time it back to back for a second or more. No counterpart in the reference: a
+ * measurement tool for the roofline's practical ceiling. out: device memory, 4-byte aligned,
+ * at least workgroups x 256 floats (out_words); its values mean nothing. FA2_EINVAL for a
+ * mode, workgroup or iteration count out of range, before any launch.
+ */
+FA2_API int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, float* out,
+                                    int64_t out_words, void* stream);
+
 /* Thread-local description of this library's last failure in this thread ("" if none). */
 FA2_API const char* fa2_ablate_last_error(void);
 

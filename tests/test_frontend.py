@@ -334,7 +334,8 @@ def test_product_library_exports_its_api_and_no_timing_variant():
 def test_measurement_library_exports_exactly_its_header():
     names = _exported(ABLATE_LIB)
     assert {n for n in names if n.startswith("fa2_")} == _c_names(ABLATE_HEADER) == {
-        "fa2_ablate_attn_fwd", "fa2_ablate_timeline", "fa2_ablate_last_error"}
+        "fa2_ablate_attn_fwd", "fa2_ablate_timeline", "fa2_ablate_mfma_ceiling",
+        "fa2_ablate_last_error"}
     # the knockouts are compiled into it: kernel instances with the no_exp, no_softmax and
     # kv_l2 bits, and matmul_only (no_softmax | kv_l2); and the timeline instance (64)
     variants = {int(m.group(1)) for n in names for m in [re.search(r"ELb[01]ELi(\d+)EEEv", n)] if m}
@@ -379,6 +380,26 @@ def test_timeline_needs_a_buffer_of_six_words_per_workgroup():
         rc = fn(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32, 32, 64, 0, 1, 1,
                 0.18, rec, words, None)
         assert rc == code and msg in lib.fa2_ablate_last_error(), (rc, lib.fa2_ablate_last_error())
+
+
+@needs_ablate
+def test_mfma_ceiling_rejects_bad_arguments_before_any_launch():
+    """fa2_ablate_mfma_ceiling checks mode, workgroup and iteration counts and its output buffer
+    (fake device pointers) without touching the GPU."""
+    import ceiling
+
+    lib, fn = ceiling._fn()
+    for mode, wg, it, out, words, code, msg in (
+            (-1, 8, 1, 0x1000, 2048, -1, b"mode"), (4, 8, 1, 0x1000, 2048, -1, b"mode"),
+            (0, 0, 1, 0x1000, 2048, -1, b"workgroups"), (0, 65537, 1, 0x1000, 1 << 30, -1, b"workgroups"),
+            (0, 8, 0, 0x1000, 2048, -1, b"iters"), (3, 8, 100001, 0x1000, 2048, -1, b"iters"),
+            (0, 8, 1, None, 2048, -1, b"null"), (1, 8, 1, 0x1002, 2048, -2, b"aligned"),
+            (2, 8, 1, 0x1000, 2047, -1, b"2048")):
+        rc = fn(mode, wg, it, out, words, None)
+        assert rc == code and msg in lib.fa2_ablate_last_error(), (mode, wg, it, rc,
+                                                                   lib.fa2_ablate_last_error())
+    assert ceiling.launch_flops(2048, 6000) == 2048 * 4 * 6000 * 16 * 32768
+    assert list(ceiling.MODES.values()) == [0, 1, 2, 3]
 
 
 def test_ablation_front_end_checks_arguments_on_the_cpu():

@@ -121,3 +121,23 @@ def test_timeline_instance_is_the_product_and_its_records_are_ordered(dtype, D, 
     for e, p, l, d, tiles, hw in recs:
         assert 0 < e <= p <= l <= d and d - e < 10**6   # under 10 ms
     assert len({decode_cu(r[5]) for r in recs}) <= 256
+
+
+def test_mfma_ceiling_probe_runs_every_mode():
+    """fa2_ablate_mfma_ceiling (triton-fa2-forward_amd/ceiling.py): one short launch per mode
+    completes and writes a finite value per lane; with constant operands (1.0) every lane's sum
+    is exact: 16 accumulator registers x 8 MFMAs per iteration x 16 products of 1.0, per
+    accumulator, twice."""
+    import ceiling
+
+    lib, fn = ceiling._fn()
+    wg, iters = 64, 10
+    stream = torch.cuda.current_stream().cuda_stream
+    for mode in ceiling.MODES.values():
+        out = torch.full((wg * 256,), float("nan"), device="cuda")
+        rc = fn(mode, wg, iters, out.data_ptr(), out.numel(), stream)
+        assert rc == 0, lib.fa2_ablate_last_error()
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all(), mode
+        if mode == ceiling.MODES["mfma_const"]:
+            assert torch.all(out == 2 * 16 * 8 * iters * 16), out[:4]

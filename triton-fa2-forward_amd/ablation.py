@@ -5,6 +5,7 @@ reference's bench/ablation.py). GPU only; a measurement tool, not part of the dr
     python triton-fa2-forward_amd/ablation.py --seqlens 8192 --dtype bf16 --rounds 5       # C3
     python triton-fa2-forward_amd/ablation.py --seqlens 16384 --batch 2 --hq 16 --hkv 16 \\
         --head-dim 64 --full --input-scale 0.5 --rounds 5                                    # C4
+    ... --sustained 2      # also each variant alone for 2 s: its rate, clock and power
 
 Every variant is the product's kernel template instantiated with VARIANT bits
 (include/fa2_ablate.h), loaded from the measurement library libfa2_ablate.so, which fa2.kernel
@@ -27,6 +28,11 @@ and clock drift hits all variants alike. The table gives each variant's median o
 spread of its rounds, and the change against `copy`. `attention()` is the shipped call on the same
 inputs; on long bf16 problems it adds the key-norm pass and that instance of the kernel (C3), which
 the variants do not have, so the deltas are taken against `copy`, not against it.
+
+With --sustained, each variant then also runs alone, back to back, with amdsmi sampling the clock
+and the socket power (sustained_run): the chip holds its power near the limit by lowering the
+clock, so a switch that saves energy also buys clock, which the interleaved rounds (one clock for
+all variants) cannot show; TFLOP/s per GHz separates the two.
 """
 
 import argparse
@@ -167,6 +173,33 @@ def interleaved_rounds(launchers, rounds, steps, warmup):
     return per_round
 
 
+def sustained_run(fn, seconds, flops):
+    """One variant alone, back to back for `seconds`, with the clock sampler beside it: the rate,
+    graphics clock and socket power it sustains. The chip holds its power near the limit by
+    lowering the clock, so work that costs energy (exp, LDS reads) also costs clock; the
+    interleaved rounds share one clock between all variants and cannot show that part."""
+    import time
+
+    import torch
+
+    import bench
+
+    fn()
+    torch.cuda.synchronize()
+    with bench.ClockSampler() as smp:
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(10):
+                fn()
+            n += 10
+            torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    clk = smp.summary()
+    return {"tflops": flops * n / dt / 1e12, "launches": n,
+            "sclk_mhz": clk.get("sclk_mhz_median"), "power_w": clk.get("power_w_median")}
+
+
 def measure_shape(args, N):
     import torch
 
@@ -205,12 +238,15 @@ def measure_shape(args, N):
     bench.settle_clocks(launchers["copy"] if "copy" in launchers else launchers["attention()"])
     per_round = interleaved_rounds(launchers, args.rounds, args.steps, args.warmup)
     base = statistics.median(per_round["copy"]) if "copy" in per_round else None
+    sustained = {name: sustained_run(fn, args.sustained, flops) for name, fn in launchers.items()} \
+        if args.sustained > 0 else {}
     rows = []
     for name, ms in per_round.items():
         med = statistics.median(ms)
         rows.append({"variant": name, "ms": med, "min_ms": min(ms), "max_ms": max(ms),
                      "vs_copy": (med / base - 1.0) if base else None,
-                     "tflops": flops / (med * 1e-3) / 1e12, **checks.get(name, {})})
+                     "tflops": flops / (med * 1e-3) / 1e12, **checks.get(name, {}),
+                     **({"sustained": sustained[name]} if name in sustained else {})})
     del q, k, v, product, shipped, outputs
     torch.cuda.empty_cache()
     return flops, rows
@@ -220,8 +256,10 @@ def print_table(args, N, rows):
     shape = (f"B={args.batch} H {args.hq}/{args.hkv} N={N} D={args.head_dim} {args.dtype} "
              f"{'full' if args.full else 'causal'}" + (f" inputs x{args.input_scale}" if args.input_scale != 1 else ""))
     print(f"\n{shape}: {args.rounds} rounds of {args.steps} back-to-back launches per variant")
-    print("| variant | ms per launch (median; min-max over rounds) | vs copy | TFLOP/s | output vs product |")
-    print("|---|---|---|---|---|")
+    sus = all("sustained" in r for r in rows)
+    print("| variant | ms per launch (median; min-max over rounds) | vs copy | TFLOP/s | output vs product |"
+          + (f" alone for {args.sustained:g} s: TFLOP/s | sclk MHz | power W | TFLOP/s per GHz |" if sus else ""))
+    print("|---|---|---|---|---|" + ("---|---|---|---|" if sus else ""))
     for r in rows:
         if r.get("bit_exact"):
             out = "bit-exact"
@@ -230,8 +268,14 @@ def print_table(args, N, rows):
         else:
             out = ""
         vs = "" if r["vs_copy"] is None or r["variant"] == "copy" else f"{r['vs_copy']:+.1%}"
+        extra = ""
+        if sus:
+            su = r["sustained"]
+            ghz = (su["sclk_mhz"] or 0) / 1000.0
+            extra = (f" {su['tflops']:.1f} | {su['sclk_mhz'] or '-'} | {su['power_w'] or '-'} | "
+                     f"{su['tflops'] / ghz:.1f} |" if ghz else f" {su['tflops']:.1f} | - | - | - |")
         print(f"| {r['variant']} | {r['ms']:.4f} ({r['min_ms']:.4f}-{r['max_ms']:.4f}) | {vs} | "
-              f"{r['tflops']:.1f} | {out} |", flush=True)
+              f"{r['tflops']:.1f} | {out} |" + extra, flush=True)
 
 
 def main():
@@ -248,6 +292,9 @@ def main():
     ap.add_argument("--rounds", type=int, default=3)
     ap.add_argument("--steps", type=int, default=20, help="back-to-back launches per variant per round")
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sustained", type=float, default=0.0, metavar="SECONDS",
+                    help="also run each variant alone for this long with amdsmi clock and power "
+                         "sampling (rate, sclk, power, rate per GHz)")
     ap.add_argument("--json", default=None, help="also write the rows here")
     args = ap.parse_args()
 

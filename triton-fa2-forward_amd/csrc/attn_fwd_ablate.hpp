@@ -50,4 +50,9 @@ FA2_DECLARE_ABLATE(1, 64)
 FA2_DECLARE_ABLATE(1, 128)
 #undef FA2_DECLARE_ABLATE
 
+// Launches mfma_ceiling_kernel<mode> (mfma_ceiling.hip) on `workgroups` workgroups of 256
+// threads, `iters` x 16 MFMAs per wave; mode is one of FA2_ABLATE_CEIL_*. Returns a hipError_t
+// value.
+int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStream_t stream);
+
 }  // namespace fa2

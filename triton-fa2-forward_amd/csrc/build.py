@@ -12,7 +12,8 @@ the plain-C host of the C ABI that the tests run (tests/capi/fa2_capi_check).
 The measurement library (include/fa2_ablate.h) is the kernel's timing variants: the same kernel
 template with work switched off, compiled from attn_fwd_ablate_inst.hip per pair and linked with
 its own C-ABI file fa2_ablate.hip into triton-fa2-forward_amd/libfa2_ablate.so, outside the
-fa2 package: the product never loads it.
+fa2 package: the product never loads it. It also holds the MFMA ceiling probe (mfma_ceiling.hip):
+what the matrix cores sustain under the chip's power limit.
 
 Both libraries are built with hidden visibility, so each exports exactly the functions its
 header declares (FA2_API). The compiler's resource report for every kernel instance (VGPRs,
@@ -125,7 +126,9 @@ def build(jobs=8, verbose=False):
            "-o", os.path.join(OBJ_DIR, "fa2_fwd.o")]
     ablate_api = [cc, *common_flags(), "-c", os.path.join(CSRC, "fa2_ablate.hip"),
                   "-o", os.path.join(OBJ_DIR, "fa2_ablate.o")]
-    everything = units + shared + [api] + ablate_units + [ablate_api]
+    ceiling = [cc, *common_flags(), "-c", os.path.join(CSRC, "mfma_ceiling.hip"),
+               "-o", os.path.join(OBJ_DIR, "mfma_ceiling.o")]
+    everything = units + shared + [api] + ablate_units + [ablate_api, ceiling]
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         errs = list(ex.map(lambda cmd: _run(cmd, verbose), everything))
 
@@ -144,7 +147,8 @@ def build(jobs=8, verbose=False):
 
     shared_objs = [u[-1] for u in shared]
     link([u[-1] for u in units] + shared_objs + [api[-1]], LIB_PATH)
-    link([u[-1] for u in ablate_units] + shared_objs + [ablate_api[-1]], ABLATE_LIB_PATH)
+    link([u[-1] for u in ablate_units] + shared_objs + [ablate_api[-1], ceiling[-1]],
+         ABLATE_LIB_PATH)
     build_capi_check(verbose)
     return LIB_PATH
 

@@ -64,4 +64,27 @@ int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
                        record_words);
 }
 
+int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, float* out,
+                            int64_t out_words, void* stream) {
+  g_err[0] = '\0';
+  if (mode < FA2_ABLATE_CEIL_MFMA || mode > FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX)
+    return fail(FA2_EINVAL, "unknown ceiling mode %d", (int)mode);
+  if (workgroups < 1 || workgroups > FA2_ABLATE_CEIL_MAX_WORKGROUPS)
+    return fail(FA2_EINVAL, "workgroups %d outside [1, %d]", (int)workgroups,
+                FA2_ABLATE_CEIL_MAX_WORKGROUPS);
+  if (iters < 1 || iters > FA2_ABLATE_CEIL_MAX_ITERS)
+    return fail(FA2_EINVAL, "iters %d outside [1, %d]", (int)iters, FA2_ABLATE_CEIL_MAX_ITERS);
+  if (!out) return fail(FA2_EINVAL, "null output");
+  if (reinterpret_cast<uintptr_t>(out) & 3u)
+    return fail(FA2_EALIGN, "the output must be 4-byte aligned");
+  if (out_words < (int64_t)workgroups * 256)
+    return fail(FA2_EINVAL, "the output holds %lld floats; %d workgroups write %lld",
+                (long long)out_words, (int)workgroups, (long long)workgroups * 256);
+  const int rc = fa2::launch_mfma_ceiling(mode, out, workgroups, iters,
+                                          static_cast<hipStream_t>(stream));
+  if (rc != 0)
+    return fail(FA2_ELAUNCH, "ceiling launch failed: %s", hipGetErrorString((hipError_t)rc));
+  return 0;
+}
+
 }  // extern "C"

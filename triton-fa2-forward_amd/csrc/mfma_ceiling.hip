@@ -1,0 +1,120 @@
+// mfma_ceiling.hip - what the matrix cores sustain on this chip, for the measurement library
+// (fa2_ablate_mfma_ceiling, include/fa2_ablate.h, checks the arguments and calls
+// launch_mfma_ceiling).
+//
+// MI355X holds its socket power near the limit by lowering the graphics clock, and the energy of
+// an MFMA depends on its operands' bits: constant operands run at the top clock, random ones do
+// not. This kernel issues v_mfma_f32_32x32x16_bf16 back to back (two independent accumulators,
+// no other dependency) in the attention kernel's launch shape: 256-thread workgroups, 64 KiB of
+// dynamic LDS each, so two workgroups (two waves per SIMD) per CU. Modes add, per MFMA, the
+// attention kernel's other work, on data that depends on nothing:
+//   FA2_ABLATE_CEIL_MFMA              random operands in registers;
+//   FA2_ABLATE_CEIL_MFMA_CONST        the same with constant operands (1.0);
+//   FA2_ABLATE_CEIL_MFMA_LDS          random operands, one 1 KiB ds_read_b128 per MFMA (the K and
+//                                     V operand traffic of 32-row waves);
+//   FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX  that plus the softmax's vector work per MFMA at head_dim
+//                                     128 (one FMA and one exp2 per score and lane register,
+//                                     half a bf16 pack, half a dot2 row sum).
+// The output is meaningless; every lane writes one float so that nothing is optimised away.
+#include <hip/hip_runtime.h>
+
+#include "attn_fwd_ablate.hpp"
+#include "attn_fwd_common.hpp"
+#include "fa2_ablate.h"
+
+namespace fa2 {
+namespace {
+
+constexpr int kCeilThreads = 256;
+constexpr size_t kCeilLdsBytes = 64 * 1024;  // two workgroups per CU, as attn_fwd_kernel
+constexpr int kCeilChunks = 16;              // operands read: 16 chunks of 1 KiB
+
+// 32-bit integer hash ("lowbias32", C. Wellons, public domain)
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// two bf16 with random sign and mantissa in +-[0.5, 2), or two 1.0
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t x, bool random) {
+  if (!random) return 0x3f803f80u;
+  const uint32_t r = mix32(x);
+  const uint32_t lo = (r & 0x8000u) | ((126u + (r >> 7 & 1u)) << 7) | (r & 0x7fu);
+  const uint32_t h = r >> 16;
+  const uint32_t hi = (h & 0x8000u) | ((126u + (h >> 7 & 1u)) << 7) | (h & 0x7fu);
+  return lo | hi << 16;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, int iters) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  constexpr bool kRandom = MODE != FA2_ABLATE_CEIL_MFMA_CONST;
+  constexpr bool kLds = MODE == FA2_ABLATE_CEIL_MFMA_LDS || MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX;
+  constexpr bool kSoftmax = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX;
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < kCeilChunks * 256; i += kCeilThreads)
+    reinterpret_cast<uint32_t*>(lds)[i] = bf16_pair(i + 4096u * blockIdx.x, kRandom);
+  __syncthreads();
+  const char FA2_LDS* chunks = (const char FA2_LDS*)lds + lane * 16;
+  const uint32_t seed = 1u << 24 | (blockIdx.x * kCeilThreads + threadIdx.x) * 4u;
+  const u32x4 b = {bf16_pair(seed, kRandom), bf16_pair(seed + 1, kRandom),
+                   bf16_pair(seed + 2, kRandom), bf16_pair(seed + 3, kRandom)};
+  u32x4 a[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = *(const volatile u32x4 FA2_LDS*)(chunks + i * 1024);
+  float sv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sv[j] = (float)(mix32(seed + 8 + j) & 0xffffu) * (1.0f / 65536.0f);
+  float lsum = 0.f, eprev = 0.f;
+  f32x16 acc0 = {}, acc1 = {};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i & 1)
+        acc1 = Elem<1>::mma(a[i & 3], b, acc1);
+      else
+        acc0 = Elem<1>::mma(a[i & 3], b, acc0);
+      // the read for the MFMA four ahead, into the register just consumed
+      if constexpr (kLds) a[i & 3] = *(const volatile u32x4 FA2_LDS*)(chunks + ((i + 4) & 15) * 1024);
+      if constexpr (kSoftmax) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i & 7], 0.0625f, -4.0f));
+        sv[i & 7] = e;
+        if (i & 1) lsum = Elem<1>::sum2(Elem<1>::pack2(eprev, e), lsum);
+        eprev = e;
+      }
+    }
+  }
+  const f32x16 s = acc0 + acc1;
+  float t = lsum;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t += s[i];
+  out[(size_t)blockIdx.x * kCeilThreads + threadIdx.x] = t;
+}
+
+template <int MODE>
+int launch_ceiling(float* out, int workgroups, int iters, hipStream_t s) {
+  hipLaunchKernelGGL(mfma_ceiling_kernel<MODE>, dim3(workgroups), dim3(kCeilThreads),
+                     kCeilLdsBytes, s, out, iters);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStream_t s) {
+  switch (mode) {
+    case FA2_ABLATE_CEIL_MFMA: return launch_ceiling<FA2_ABLATE_CEIL_MFMA>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_MFMA_CONST:
+      return launch_ceiling<FA2_ABLATE_CEIL_MFMA_CONST>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_MFMA_LDS:
+      return launch_ceiling<FA2_ABLATE_CEIL_MFMA_LDS>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX:
+      return launch_ceiling<FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX>(out, workgroups, iters, s);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fa2
