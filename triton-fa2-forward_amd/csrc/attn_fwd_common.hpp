@@ -192,8 +192,8 @@ __device__ __forceinline__ u32x4 make_desc(const void* base, uint32_t bytes) {
 }
 
 // LDS byte address of a __shared__ object, as a wave-uniform value.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const FA2_LDS void*)p);
+__device__ __forceinline__ uint32_t lds_addr(const FA2_LDS void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
 
 // 16 bytes HBM -> LDS without VGPRs: lane l of the wave writes lds_base + 16 * l

@@ -211,7 +211,7 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
       const int j = wave + jj * NW;
-      if (NI % NW == 0 || j < NI) load_lds16(rs, koff[jj], lds_addr(&k_lds[buf][j * 64]));
+      if (NI % NW == 0 || j < NI) load_lds16(rs, koff[jj], lds_addr((const FA2_LDS char*)k_lds[buf] + j * 64 * 16));
     }
   };
   auto issue_v = [&](int n0, int buf) {
@@ -219,7 +219,7 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
       const int j = wave + jj * NW;
-      if (NI % NW == 0 || j < NI) load_lds16(rs, voff[jj], lds_addr(&v_lds[buf][j * 64]));
+      if (NI % NW == 0 || j < NI) load_lds16(rs, voff[jj], lds_addr((const FA2_LDS char*)v_lds[buf] + j * 64 * 16));
     }
   };
 
