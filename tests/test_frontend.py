@@ -390,7 +390,7 @@ def test_mfma_ceiling_rejects_bad_arguments_before_any_launch():
 
     lib, fn = ceiling._fn()
     for mode, wg, it, out, words, code, msg in (
-            (-1, 8, 1, 0x1000, 2048, -1, b"mode"), (4, 8, 1, 0x1000, 2048, -1, b"mode"),
+            (-1, 8, 1, 0x1000, 2048, -1, b"mode"), (6, 8, 1, 0x1000, 2048, -1, b"mode"),
             (0, 0, 1, 0x1000, 2048, -1, b"workgroups"), (0, 65537, 1, 0x1000, 1 << 30, -1, b"workgroups"),
             (0, 8, 0, 0x1000, 2048, -1, b"iters"), (3, 8, 100001, 0x1000, 2048, -1, b"iters"),
             (0, 8, 1, None, 2048, -1, b"null"), (1, 8, 1, 0x1002, 2048, -2, b"aligned"),
@@ -399,7 +399,7 @@ def test_mfma_ceiling_rejects_bad_arguments_before_any_launch():
         assert rc == code and msg in lib.fa2_ablate_last_error(), (mode, wg, it, rc,
                                                                    lib.fa2_ablate_last_error())
     assert ceiling.launch_flops(2048, 6000) == 2048 * 4 * 6000 * 16 * 32768
-    assert list(ceiling.MODES.values()) == [0, 1, 2, 3]
+    assert list(ceiling.MODES.values()) == [0, 1, 2, 3, 4, 5]
 
 
 def test_ablation_front_end_checks_arguments_on_the_cpu():

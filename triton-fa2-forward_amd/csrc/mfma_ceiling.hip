@@ -14,7 +14,10 @@
 //                                     V operand traffic of 32-row waves);
 //   FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX  that plus the softmax's vector work per MFMA at head_dim
 //                                     128 (one FMA and one exp2 per score and lane register,
-//                                     half a bf16 pack, half a dot2 row sum).
+//                                     half a bf16 pack, half a dot2 row sum);
+//   FA2_ABLATE_CEIL_MFMA_EXP          random operands in registers, one exp2 per MFMA;
+//   FA2_ABLATE_CEIL_MFMA_FMA2         random operands in registers, two FMAs per MFMA
+// (the last two price an exp2 against FMAs in the issue cycles beside the MFMAs).
 // The output is meaningless; every lane writes one float so that nothing is optimised away.
 #include <hip/hip_runtime.h>
 
@@ -55,6 +58,8 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
   constexpr bool kRandom = MODE != FA2_ABLATE_CEIL_MFMA_CONST;
   constexpr bool kLds = MODE == FA2_ABLATE_CEIL_MFMA_LDS || MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX;
   constexpr bool kSoftmax = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX;
+  constexpr bool kExp = MODE == FA2_ABLATE_CEIL_MFMA_EXP;
+  constexpr bool kFma2 = MODE == FA2_ABLATE_CEIL_MFMA_FMA2;
   const int lane = threadIdx.x & 63;
   for (int i = threadIdx.x; i < kCeilChunks * 256; i += kCeilThreads)
     reinterpret_cast<uint32_t*>(lds)[i] = bf16_pair(i + 4096u * blockIdx.x, kRandom);
@@ -86,10 +91,19 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
         if (i & 1) lsum = Elem<1>::sum2(Elem<1>::pack2(eprev, e), lsum);
         eprev = e;
       }
+      if constexpr (kExp) sv[i & 7] = __builtin_amdgcn_exp2f(sv[i & 7] * -1.0f);
+      if constexpr (kFma2) {
+        sv[i & 7] = __builtin_fmaf(sv[i & 7], 0.9990234375f, 0.0009765625f);
+        sv[(i + 4) & 7] = __builtin_fmaf(sv[(i + 4) & 7], 0.9990234375f, 0.0009765625f);
+      }
     }
   }
   const f32x16 s = acc0 + acc1;
   float t = lsum;
+  if constexpr (kExp || kFma2) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t += sv[j];
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i) t += s[i];
   out[(size_t)blockIdx.x * kCeilThreads + threadIdx.x] = t;
@@ -113,6 +127,10 @@ int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStre
       return launch_ceiling<FA2_ABLATE_CEIL_MFMA_LDS>(out, workgroups, iters, s);
     case FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX:
       return launch_ceiling<FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_MFMA_EXP:
+      return launch_ceiling<FA2_ABLATE_CEIL_MFMA_EXP>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_MFMA_FMA2:
+      return launch_ceiling<FA2_ABLATE_CEIL_MFMA_FMA2>(out, workgroups, iters, s);
     default: return (int)hipErrorInvalidValue;
   }
 }
