@@ -196,6 +196,24 @@ def test_oracle_on_gpu_matches_oracle_on_cpu():
 
 
 # ------------------------------------------------------------------------------------------
+# Causal program order: when the (batch, kv head) units split evenly over the 8 XCDs, each XCD
+# runs them a chunk at a time (the host picks the chunk from the units' K/V bytes: 3 of 6, 4 of
+# 12, 2 of 8 and 4 of 8 units below); every program must still run exactly once
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,H_q,H_kv,N,dtype,pack", [
+    (3, 16, 16, 4096, torch.bfloat16, False),   # 6 units per XCD, chunks of 3
+    (6, 16, 16, 4096, torch.float16, False),    # 12 per XCD, chunks of 4
+    (2, 32, 32, 8192, torch.bfloat16, False),   # 8 per XCD, 4 MiB units: chunks of 2
+    (8, 32, 8, 4096, torch.bfloat16, True),     # packed GQA, 8 per XCD, chunks of 4
+])
+def test_causal_unit_chunks(B, H_q, H_kv, N, dtype, pack):
+    q, k, v = make_qkv(B, H_q, H_kv, N, N, 128, dtype)
+    out = _attention()(q, k, v, causal=True, pack_gqa=pack)
+    check_against_oracle(q, k, v, True, precision=torch.float32, ours=out)
+
+
+# ------------------------------------------------------------------------------------------
 # 32-key tiles under 128- and 256-row programs (4 and 8 waves)
 # ------------------------------------------------------------------------------------------
 

@@ -23,8 +23,6 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 #define FA2_LDS __attribute__((address_space(3)))
 #define FA2_GLOBAL __attribute__((address_space(1)))
 
-// Number of XCDs (each with its own L2) that the hardware deals workgroups to round-robin.
-constexpr int kXcds = 8;
 // Compute units (8 XCDs x 32). With two workgroups per CU, the dispatcher's first round places
 // block b and block b + kCus on the same CU (measured with the hardware CU id).
 constexpr int kCus = 256;
@@ -252,10 +250,17 @@ __device__ __forceinline__ Program program_of(const Params& p, int block) {
     const int xcd = block % kXcds, slot = block / kXcds;
     const int upx = units / kXcds;             // units per XCD
     if (CAUSAL) {
-      const int per_t = upx * progs_per_kv;    // programs per q tile on one XCD
-      t = slot / per_t;
-      const int r = slot - t * per_t;
-      kv_index = xcd * upx + r / progs_per_kv; // b * h_kv + hkv
+      // the XCD's units are taken unit_chunk at a time (the host's choice, a divisor of upx),
+      // q-tile-major inside each chunk: heavy tiles first, and the programs in flight read the
+      // K/V of a few units instead of all of the XCD's
+      const int cu = (p.unit_chunk > 0 && upx % p.unit_chunk == 0) ? p.unit_chunk : upx;
+      const int per_chunk = cu * progs_per_kv * p.n_tiles;  // programs of one chunk
+      const int ch = slot / per_chunk;
+      const int rs = slot - ch * per_chunk;
+      const int per_t = cu * progs_per_kv;     // programs per q tile of one chunk
+      t = rs / per_t;
+      const int r = rs - t * per_t;
+      kv_index = xcd * upx + ch * cu + r / progs_per_kv; // b * h_kv + hkv
       h_in = r % progs_per_kv;
     } else {
       // every program has the same work: unit after unit, so that the XCD's programs in flight

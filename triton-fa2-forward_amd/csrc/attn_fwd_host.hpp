@@ -99,6 +99,23 @@ bool key_table_pays(int64_t batch, int64_t h_q, int64_t h_kv, int64_t n_q, int64
   return kbytes > 0 && flops >= 16384.0 * kbytes && flops >= 137438953472.0;  // 2^37
 }
 
+// Causal programs on one XCD (program_of): its (batch, kv head) units are taken a chunk at a
+// time, q-tile-major inside the chunk, so that the programs in flight read the K/V of at most
+// ~kChunkKvBytes of units. Measured on MI355X against all of the XCD's units at once (causal,
+// bf16 unless stated; 2, 3 or 4 units per chunk): B8 H16 N4096 D128 +4.9% (4), B2 H32 N8192
+// D128 +2.4% (2), C2 (B4 H16 N4096) +0.5% (4); at head_dim 64 (fp16 B4 H16 N4096) chunks of 4
+// and 2 lost 4% and 9%, which the byte budget avoids (1 MiB units: all 8 at once).
+constexpr int64_t kChunkKvBytes = int64_t(8) << 20;
+int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim) {
+  const int64_t upx = units / fa2::kXcds;
+  if (upx < 1) return 1;
+  const int64_t unit_kv = 4 * n_kv * head_dim;  // K and V bytes of one unit
+  int64_t chunk = unit_kv > 0 ? std::max<int64_t>(1, kChunkKvBytes / unit_kv) : upx;
+  if (chunk >= upx) return (int32_t)upx;
+  while (upx % chunk) --chunk;
+  return (int32_t)chunk;
+}
+
 // Launches the attention kernel of one checked call: the product's instances in the library,
 // the timing variants (variant != 0) in the measurement library. Returns a hipError_t value.
 using KernelLaunch = int (*)(int dtype, int di, const Params& p, int waves, int block_n,
@@ -209,6 +226,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
                 (long long)rows, block_m);
   p.n_tiles = (int32_t)n_tiles;
   p.n_bh = (int32_t)n_bh;
+  p.unit_chunk = unit_chunk(n_bh / (group / pack), n_kv, head_dim);
   p.qk_scale = qk_scale;
   p.lse = lse;
   p.part_o = nullptr;

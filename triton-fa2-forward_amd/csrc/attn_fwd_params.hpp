@@ -5,6 +5,9 @@
 
 namespace fa2 {
 
+// Number of XCDs (each with its own L2) that the hardware deals workgroups to round-robin.
+constexpr int kXcds = 8;
+
 // Keys per entry of the key-norm table (attn_key_norm.hip): one workgroup of the key-norm pass
 // each (C3: 1024 workgroups), and at most three entries per 128-row causal program's own rows.
 constexpr int kKeyChunk = 64;
@@ -26,6 +29,9 @@ struct Params {
   int32_t block_m;  // (position, head) rows per program
   int32_t n_tiles;  // programs along the packed rows: ceil(n_q * pack / block_m)
   int32_t n_bh;     // programs along batch x head groups: batch * h_q / pack
+  // Causal grids whose (batch, kv head) units split evenly over the XCDs: each XCD runs its
+  // units unit_chunk at a time (a divisor of its unit count), q-tile-major inside a chunk.
+  int32_t unit_chunk;
   float qk_scale;   // sm_scale * log2(e)
   // Optional outputs beyond the reference's:
   float* lse;        // [B, H_q, N_q] natural-log log-sum-exp of the scaled scores, or null;
