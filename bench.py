@@ -630,7 +630,8 @@ def main():
                     help="instead of C3: the reference's few-queries table, one line per N_q")
     ap.add_argument("--flush-iters", type=int, default=10, help="iterations of the flushed pass (0: skip)")
     ap.add_argument("--no-ceiling", action="store_true",
-                    help="skip the measured MFMA ceiling (fa2_ablate_mfma_ceiling, ~3 s)")
+                    help="skip the measured ceilings (fa2_ablate_mfma_ceiling, ~3 s; with "
+                         "--pack-short fa2_ablate_hbm_read, ~5 s)")
     ap.add_argument("--sdpa", action="store_true",
                     help="also time torch's fused SDPA on the same inputs (sdpa_same_box, context)")
     args = ap.parse_args()
@@ -647,8 +648,32 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs the GPU")
     if args.pack_short:
+        hbm = None
+        if not args.no_ceiling:
+            try:
+                import ceiling
+
+                kv_mib = (2 * PACK_SHORT["B"] * PACK_SHORT["H_kv"] * PACK_SHORT["N_kv"]
+                          * PACK_SHORT["D"] * 2) >> 20
+                hbm = {"hbm_2gib": ceiling.measure_hbm_read(1.0, 2048),
+                       "same_size_as_kv": ceiling.measure_hbm_read(1.0, kv_mib)}
+                hbm["gbs"] = hbm["same_size_as_kv"]["gbs"]
+                hbm["source"] = ("fa2_ablate_hbm_read (libfa2_ablate.so, csrc/mfma_ceiling.hip): a "
+                                 "streaming read, back to back, best grid size, of a 2 GiB buffer "
+                                 "(past the 256 MiB Infinity Cache: HBM) and of one the size of "
+                                 f"K + V ({kv_mib} MiB, partly cache-resident when read back to back, "
+                                 "as the attention's K/V are here); the fraction is against the "
+                                 "latter")
+            except Exception as e:  # noqa: BLE001
+                hbm = {"error": f"{type(e).__name__}: {e}"}
         for n_q in sorted(PACK_SHORT_H100_US):
-            print(json.dumps(run_pack_short(n_q, args.steps, args.warmup)), flush=True)
+            res = run_pack_short(n_q, args.steps, args.warmup)
+            if hbm is not None:
+                res["roofline"]["measured_ceiling"] = hbm
+                if hbm.get("gbs"):
+                    res["roofline"]["frac_of_measured_read_rate"] = round(
+                        res["roofline"]["achieved"] / hbm["gbs"], 4)
+            print(json.dumps(res), flush=True)
         return
     names = ["C3", "C2", "C4", "C5"] if args.all else [args.config]
     ceil = None if args.no_ceiling else measured_ceiling()

@@ -107,6 +107,17 @@ FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, voi
 FA2_API int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, float* out,
                                     int64_t out_words, void* stream);
 
+/*
+ * fa2_ablate_hbm_read - the memory-side ceiling: workgroups x 256 threads read `bytes` of src
+ * (16 bytes per lane per load, four loads in flight per lane, grid-stride) and each thread writes
+ * one word of out (meaningless). Time it back to back over a buffer far larger than the caches
+ * (the Infinity Cache holds 256 MiB) for the read rate HBM sustains. No counterpart in the
+ * reference: a measurement tool for the few-queries regime's roofline. src: 16-byte aligned,
+ * bytes a positive multiple of 16; out: 4-byte aligned, at least workgroups x 256 words.
+ */
+FA2_API int fa2_ablate_hbm_read(const void* src, int64_t bytes, uint32_t* out, int64_t out_words,
+                                int32_t workgroups, void* stream);
+
 /* Thread-local description of this library's last failure in this thread ("" if none). */
 FA2_API const char* fa2_ablate_last_error(void);
 

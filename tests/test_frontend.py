@@ -335,7 +335,7 @@ def test_measurement_library_exports_exactly_its_header():
     names = _exported(ABLATE_LIB)
     assert {n for n in names if n.startswith("fa2_")} == _c_names(ABLATE_HEADER) == {
         "fa2_ablate_attn_fwd", "fa2_ablate_timeline", "fa2_ablate_mfma_ceiling",
-        "fa2_ablate_last_error"}
+        "fa2_ablate_hbm_read", "fa2_ablate_last_error"}
     # the knockouts are compiled into it: kernel instances with the no_exp, no_softmax and
     # kv_l2 bits, and matmul_only (no_softmax | kv_l2); and the timeline instance (64)
     variants = {int(m.group(1)) for n in names for m in [re.search(r"ELb[01]ELi(\d+)EEEv", n)] if m}
@@ -399,6 +399,16 @@ def test_mfma_ceiling_rejects_bad_arguments_before_any_launch():
         assert rc == code and msg in lib.fa2_ablate_last_error(), (mode, wg, it, rc,
                                                                    lib.fa2_ablate_last_error())
     assert ceiling.launch_flops(2048, 6000) == 2048 * 4 * 6000 * 16 * 32768
+    rd = lib.fa2_ablate_hbm_read
+    rd.restype = ctypes.c_int
+    rd.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                   ctypes.c_void_p]
+    for src, nb, out, words, wg, code, msg in (
+            (None, 1024, 0x1000, 256, 1, -1, b"null"), (0x1008, 1024, 0x1000, 256, 1, -2, b"aligned"),
+            (0x1000, 1000, 0x2000, 256, 1, -1, b"multiple of 16"), (0x1000, 1024, 0x2000, 256, 0, -1, b"workgroups"),
+            (0x1000, 1024, 0x2000, 511, 2, -1, b"512")):
+        rc = rd(src, nb, out, words, wg, None)
+        assert rc == code and msg in lib.fa2_ablate_last_error(), (src, nb, rc, lib.fa2_ablate_last_error())
     assert list(ceiling.MODES.values()) == [0, 1, 2, 3, 4, 5]
 
 

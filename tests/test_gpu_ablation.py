@@ -141,3 +141,34 @@ def test_mfma_ceiling_probe_runs_every_mode():
         assert torch.isfinite(out).all(), mode
         if mode == ceiling.MODES["mfma_const"]:
             assert torch.all(out == 2 * 16 * 8 * iters * 16), out[:4]
+
+
+def test_hbm_read_probe_reads_every_word():
+    """fa2_ablate_hbm_read: every word of the buffer is read once: the XOR of the per-thread
+    outputs equals the XOR of the buffer's 32-bit words (grid-stride loop, unrolled by four, and
+    its tail), on a size that is not a multiple of the grid's stride."""
+    import ctypes
+
+    from ablation import ablate_lib
+
+    lib = ablate_lib()
+    rd = lib.fa2_ablate_hbm_read
+    rd.restype = ctypes.c_int
+    rd.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                   ctypes.c_void_p]
+    g = torch.Generator(device="cpu").manual_seed(3)
+    words = torch.randint(-2**31, 2**31 - 1, (16 * 12345,), generator=g, dtype=torch.int64).to(torch.int32)
+    src = words.cuda()
+    for wg in (1, 7, 64):
+        out = torch.zeros(wg * 256, dtype=torch.int32, device="cuda")
+        rc = rd(src.data_ptr(), src.numel() * 4, out.data_ptr(), out.numel(), wg,
+                torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.fa2_ablate_last_error()
+        torch.cuda.synchronize()
+        want = 0
+        for w in words.tolist():
+            want ^= w & 0xFFFFFFFF
+        got = 0
+        for w in out.cpu().tolist():
+            got ^= w & 0xFFFFFFFF
+        assert got == want, wg

@@ -21,6 +21,11 @@ amdsmi sampling the clock and the socket power:
 
 Per mode: TFLOP/s, the median graphics clock and power, TFLOP/s per GHz (the issue efficiency,
 whatever the clock: the peak is 1048.6 per GHz) and the fraction of the 2.4 GHz peak.
+
+--hbm adds the memory-side ceiling (fa2_ablate_hbm_read): a streaming read, back to back, 16
+bytes per lane per load, at a few grid sizes, against the 8 TB/s HBM peak, of a 2 GiB buffer (far
+past the 256 MiB Infinity Cache: what HBM sustains) and of 256 and 64 MiB buffers (partly or
+wholly cache-resident when read back to back).
 """
 
 import argparse
@@ -95,10 +100,53 @@ def measure(mode, seconds=2.0, warm_s=0.5, workgroups=WORKGROUPS, iters=ITERS):
             "seconds": round(dt, 2)}
 
 
+HBM_PEAK_GBS = 8000.0
+
+
+def measure_hbm_read(seconds=1.0, mib=2048, workgroups=(1024, 2048, 4096, 8192)):
+    """Streaming read of a `mib` MiB buffer back to back for `seconds` per grid size: {workgroups:
+    GB/s} and the best, in GB/s and as a fraction of the 8 TB/s peak."""
+    import torch
+
+    import ablation
+
+    lib = ablation.ablate_lib()
+    fn = lib.fa2_ablate_hbm_read
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                   ctypes.c_void_p]
+    nbytes = mib << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 256)
+    out = torch.empty(max(workgroups) * 256, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    rates = {}
+    for wg in workgroups:
+        def launch():
+            rc = fn(src.data_ptr(), nbytes, out.data_ptr(), out.numel(), wg, stream)
+            if rc != 0:
+                raise RuntimeError(lib.fa2_ablate_last_error().decode(errors="replace"))
+        for _ in range(3):
+            launch()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(5):
+                launch()
+            n += 5
+            torch.cuda.synchronize()
+        rates[wg] = round(nbytes * n / (time.perf_counter() - t0) / 1e9, 1)
+    best = max(rates.values())
+    del src
+    return {"gbs_by_workgroups": rates, "gbs": best, "frac_of_peak": round(best / HBM_PEAK_GBS, 4),
+            "buffer_mib": mib}
+
+
 def main():
     ap = argparse.ArgumentParser(description="sustained MFMA rate under the chip's power limit")
     ap.add_argument("--seconds", type=float, default=2.0)
     ap.add_argument("--modes", nargs="+", default=list(MODES), choices=list(MODES))
+    ap.add_argument("--hbm", action="store_true", help="also the streaming HBM read rate")
     args = ap.parse_args()
 
     import torch
@@ -115,6 +163,14 @@ def main():
         r = rows[m] = measure(m, args.seconds)
         print(f"| {m} | {r['tflops']:.0f} | {r['sclk_mhz']} | {r['power_w']} | "
               f"{r['tflops_per_ghz']} | {100 * r['frac_of_peak']:.1f} |", flush=True)
+    if args.hbm:
+        print()
+        for mib in (2048, 256, 64):
+            h = measure_hbm_read(args.seconds / 2, mib)
+            print(f"streaming read of {h['buffer_mib']} MiB (fa2_ablate_hbm_read): "
+                  + ", ".join(f"{wg} workgroups {gbs:.0f} GB/s" for wg, gbs in h["gbs_by_workgroups"].items())
+                  + f"; best {h['gbs']:.0f} GB/s = {100 * h['frac_of_peak']:.1f}% of 8 TB/s", flush=True)
+            rows[f"hbm_read_{mib}mib"] = h
     return rows
 
 

@@ -55,4 +55,8 @@ FA2_DECLARE_ABLATE(1, 128)
 // value.
 int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStream_t stream);
 
+// Launches hbm_read_kernel (mfma_ceiling.hip): `workgroups` x 256 threads read n16 16-byte words
+// of src, grid-stride, each thread writing one word of out. Returns a hipError_t value.
+int launch_hbm_read(const void* src, int64_t n16, uint32_t* out, int workgroups, hipStream_t stream);
+
 }  // namespace fa2

@@ -87,4 +87,23 @@ int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, flo
   return 0;
 }
 
+int fa2_ablate_hbm_read(const void* src, int64_t bytes, uint32_t* out, int64_t out_words,
+                        int32_t workgroups, void* stream) {
+  g_err[0] = '\0';
+  if (!src || !out) return fail(FA2_EINVAL, "null buffer");
+  if ((reinterpret_cast<uintptr_t>(src) & 15u) || (reinterpret_cast<uintptr_t>(out) & 3u))
+    return fail(FA2_EALIGN, "src must be 16-byte and out 4-byte aligned");
+  if (bytes < 16 || bytes % 16) return fail(FA2_EINVAL, "bytes (%lld) must be a positive multiple of 16", (long long)bytes);
+  if (workgroups < 1 || workgroups > FA2_ABLATE_CEIL_MAX_WORKGROUPS)
+    return fail(FA2_EINVAL, "workgroups %d outside [1, %d]", (int)workgroups,
+                FA2_ABLATE_CEIL_MAX_WORKGROUPS);
+  if (out_words < (int64_t)workgroups * 256)
+    return fail(FA2_EINVAL, "the output holds %lld words; %d workgroups write %lld",
+                (long long)out_words, (int)workgroups, (long long)workgroups * 256);
+  const int rc = fa2::launch_hbm_read(src, bytes / 16, out, workgroups, static_cast<hipStream_t>(stream));
+  if (rc != 0)
+    return fail(FA2_ELAUNCH, "read launch failed: %s", hipGetErrorString((hipError_t)rc));
+  return 0;
+}
+
 }  // extern "C"

@@ -19,6 +19,10 @@
 //   FA2_ABLATE_CEIL_MFMA_FMA2         random operands in registers, two FMAs per MFMA
 // (the last two price an exp2 against FMAs in the issue cycles beside the MFMAs).
 // The output is meaningless; every lane writes one float so that nothing is optimised away.
+//
+// hbm_read_kernel is the memory-side counterpart (fa2_ablate_hbm_read): a streaming read of a
+// buffer, 16 bytes per lane per load, four loads in flight per lane, grid-stride, for the rate
+// HBM sustains on a plain read (the bound of the few-queries, split-KV regime).
 #include <hip/hip_runtime.h>
 
 #include "attn_fwd_ablate.hpp"
@@ -116,7 +120,26 @@ int launch_ceiling(float* out, int workgroups, int iters, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
+__global__ __launch_bounds__(kCeilThreads) void hbm_read_kernel(const u32x4* src, int64_t n16,
+                                                                uint32_t* out) {
+  const int64_t stride = (int64_t)gridDim.x * kCeilThreads;
+  int64_t i = (int64_t)blockIdx.x * kCeilThreads + threadIdx.x;
+  u32x4 x = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    x ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) x ^= src[i];
+  out[(int64_t)blockIdx.x * kCeilThreads + threadIdx.x] = x[0] ^ x[1] ^ x[2] ^ x[3];
+}
+
 }  // namespace
+
+int launch_hbm_read(const void* src, int64_t n16, uint32_t* out, int workgroups, hipStream_t s) {
+  hipLaunchKernelGGL(hbm_read_kernel, dim3(workgroups), dim3(kCeilThreads), 0, s,
+                     static_cast<const u32x4*>(src), n16, out);
+  return (int)hipGetLastError();
+}
 
 int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStream_t s) {
   switch (mode) {
