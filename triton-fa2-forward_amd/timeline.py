@@ -73,23 +73,60 @@ def decode_cu(hw):
     return xcc, (hw_id >> 13) & 0x7, (hw_id >> 12) & 1, (hw_id >> 8) & 0xF
 
 
-def summarize(recs, flops=None):
+def rows_of(recs):
+    """Per-workgroup rows (times in us from the first entry) of raw timeline records."""
     t0 = min(r[0] for r in recs)
     rows = []
     for b, (e, p, l, d, tiles, hw) in enumerate(recs):
         rows.append({"block": b, "start": (e - t0) * TICK_US, "prologue": (p - e) * TICK_US,
                      "loop": (l - p) * TICK_US, "epilogue": (d - l) * TICK_US,
                      "end": (d - t0) * TICK_US, "tiles": tiles, "cu": decode_cu(hw)})
+    return rows
+
+
+def rows_from_csv(path):
+    """The rows main() --csv wrote (to summarise a saved run again)."""
+    rows = []
+    with open(path) as f:
+        next(f)
+        for line in f:
+            v = line.strip().split(",")
+            rows.append({"block": int(v[0]), "start": float(v[1]), "prologue": float(v[2]),
+                         "loop": float(v[3]), "epilogue": float(v[4]), "end": float(v[5]),
+                         "tiles": int(v[6]), "cu": tuple(int(x) for x in v[7:11])})
+    return rows
+
+
+def slots_per_cu(rows):
+    """The most workgroups resident on one CU at once (two at head_dim 128, three at 64)."""
+    best = 0
+    by_cu = collections.defaultdict(list)
+    for r in rows:
+        by_cu[r["cu"]].append(r)
+    for g in by_cu.values():
+        ev = sorted([(r["start"], 1) for r in g] + [(r["end"], -1) for r in g])
+        cur = 0
+        for _, d in ev:
+            cur += d
+            best = max(best, cur)
+    return best
+
+
+def summarize(recs, flops=None):
+    return summarize_rows(rows_of(recs), flops)
+
+
+def summarize_rows(rows, flops=None):
     span = max(r["end"] for r in rows)
     cus = collections.defaultdict(list)
     for r in rows:
         cus[r["cu"]].append(r)
     busy = sum(r["end"] - r["start"] for r in rows)
-    slots = 2 * len(cus)
+    slots = slots_per_cu(rows) * len(cus)
     lines = [f"workgroups {len(rows)} on {len(cus)} CUs; span {span:.2f} us"
              + (f" ({flops / (span * 1e-6) / 1e12:.0f} TFLOP/s over the span)" if flops else ""),
              f"resident workgroup-time {busy:.0f} us = {100 * busy / (slots * span):.1f}% of "
-             f"{slots} slots x span; summed prologue {sum(r['prologue'] for r in rows):.0f} us, "
+             f"{slots} slots ({slots // len(cus)} per CU) x span; summed prologue {sum(r['prologue'] for r in rows):.0f} us, "
              f"loop {sum(r['loop'] for r in rows):.0f} us, epilogue {sum(r['epilogue'] for r in rows):.0f} us",
              "", "| tiles | workgroups | start (us, min-median-max) | prologue us (median) | loop us (median) "
              "| us per tile | epilogue us (median) | end (us, median-max) |", "|---|---|---|---|---|---|---|---|"]
@@ -133,7 +170,14 @@ def main():
     ap.add_argument("--config", default="C5")
     ap.add_argument("--launches", type=int, default=20, help="launches before the recorded one")
     ap.add_argument("--csv", default=None, help="also write the per-workgroup rows here")
+    ap.add_argument("--from-csv", default=None, help="summarise rows a previous --csv wrote (no GPU)")
     args = ap.parse_args()
+    if args.from_csv:
+        import bench
+
+        dt, causal, B, hq, hkv, n, d, scale, outl = bench.WORKLOADS[args.config]
+        print(summarize_rows(rows_from_csv(args.from_csv), bench.attn_flops(B, hq, n, n, d, causal))[1])
+        return
 
     import torch
 
