@@ -186,13 +186,20 @@ def sustained_run(fn, seconds, flops):
 
     fn()
     torch.cuda.synchronize()
+    # launches per synchronize: ~20 ms of work, so that short kernels (C5: ~30 us) are not timed
+    # with a host round trip every few hundred microseconds
+    t0 = time.perf_counter()
+    for _ in range(10):
+        fn()
+    torch.cuda.synchronize()
+    batch = max(10, int(0.02 / max((time.perf_counter() - t0) / 10, 1e-6)))
     with bench.ClockSampler() as smp:
         t0 = time.perf_counter()
         n = 0
         while time.perf_counter() - t0 < seconds:
-            for _ in range(10):
+            for _ in range(batch):
                 fn()
-            n += 10
+            n += batch
             torch.cuda.synchronize()
         dt = time.perf_counter() - t0
     clk = smp.summary()
