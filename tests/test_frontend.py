@@ -483,6 +483,23 @@ def test_build_records_the_resources_of_every_product_instance():
 
 
 @needs_lib
+def test_default_instances_keep_the_occupancy_the_design_counts_on():
+    """The compiler's report of the default instances: two waves per SIMD and no VGPR spills at
+    head_dim 128 (C2, C3, C5; with and without the key-norm table), three waves per SIMD and no
+    VGPR spills for the fp16 head_dim-64 software-pipelined instance (C4)."""
+    import sweep
+
+    res = sweep.load_resources()
+    for dt in (0, 1):
+        for causal in (False, True):
+            for keynorm in (False, True):
+                r = res[sweep.instance_name(dt, 128, 128, 64, causal, keynorm)]
+                assert r["waves_per_simd"] >= 2 and r["vgpr_spills"] == 0, r
+    r = res[sweep.instance_name(0, 64, 128, 64, False, False)]
+    assert r["waves_per_simd"] == 3 and r["vgpr_spills"] == 0, r
+
+
+@needs_lib
 def test_fa2_installs_as_a_package(tmp_path):
     """`pip install .` puts the drop-in under its reference import name with the built library
     inside, so `from fa2.kernel import
