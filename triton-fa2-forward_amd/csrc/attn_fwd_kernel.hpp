@@ -238,6 +238,10 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
     koffs[ks] = (uint32_t)((pi_row(c) * CPR + ((2 * ks + g) ^ kk)) * 16);
+  // Kept whole: split into a shared part and a per-k-step part, each read's address would cost
+  // two vector instructions per tile (or, add) instead of one (or with the buffer base).
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(koffs[ks]));
   uint32_t voffs[2][DB];
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr)
