@@ -201,10 +201,15 @@ void attn_fwd_kernel(const Params p) {
     koff[jj] = (uint32_t)(row * p.skn + (col ^ k_key<D>(pi_row(row & 31) & 15)) * 8) * 2u;
     voff[jj] = (uint32_t)(row * p.svn + (col ^ v_key<D>(row & 15)) * 8) * 2u;
   }
+  // The resource of the tile at key n0 covers its rows n0 .. min(n0 + BN, n_kv) - 1 only (the
+  // loads touch no other row). The host keeps a row stride below 2^22 elements, so its byte
+  // stride and (BN - 1) rows of it plus a row's D elements stay below 2^31: 32-bit products, the
+  // 64-bit base added once (n0 >= 0, and n0 < n_kv since only tiles of the range are issued).
   auto rsrc_at = [&](const char* base, int64_t stride, int n0) {
-    const int64_t rows_left = p.n_kv - n0;  // >= 1
-    const int64_t bytes = ((rows_left - 1) * stride + D) * 2;
-    return make_desc(base + (int64_t)n0 * stride * 2, (uint32_t)min(bytes, (int64_t)0x7fffffff));
+    const uint32_t stride2 = (uint32_t)stride * 2u;
+    const uint32_t rows = (uint32_t)min(p.n_kv - n0, BN);  // 1 .. BN
+    const uint32_t bytes = (rows - 1u) * stride2 + (uint32_t)D * 2u;
+    return make_desc(base + (uint64_t)(uint32_t)n0 * stride2, bytes);
   };
   auto issue_k = [&](int n0, int buf) {
     const auto rs = rsrc_at(kbase, p.skn, kKvL2 ? kv_begin : n0);
