@@ -448,12 +448,15 @@ def sustained_clock(fn, seconds=1.0):
 def measured_ceiling(seconds=1.0):
     """The MFMA rate this box sustains under its power limit (triton-fa2-forward_amd/ceiling.py,
     fa2_ablate_mfma_ceiling in the measurement library): bf16 MFMAs on random operands alone, and
-    with the attention kernel's LDS operand reads and softmax vector work beside them. The nominal
-    peak assumes 2.4 GHz; on random data the chip holds its power by running lower."""
+    with the attention kernel's LDS operand reads and softmax vector work beside them, with the
+    accumulators in AGPRs (the compiler's choice for the probe) and in VGPRs (where the attention
+    kernel keeps them). The nominal peak assumes 2.4 GHz; on random data the chip holds its power
+    by running lower."""
     try:
         import ceiling
 
-        out = {m: ceiling.measure(m, seconds) for m in ("mfma", "mfma_lds_softmax")}
+        out = {m: ceiling.measure(m, seconds)
+               for m in ("mfma", "mfma_lds_softmax", "mfma_lds_softmax_vacc")}
     except Exception as e:  # noqa: BLE001
         return {"error": f"{type(e).__name__}: {e}"}
     out["source"] = ("fa2_ablate_mfma_ceiling (libfa2_ablate.so, csrc/mfma_ceiling.hip), "
@@ -553,6 +556,9 @@ def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False, ceiling=Non
         mix = ceiling.get("mfma_lds_softmax", {}).get("tflops")
         res["roofline"]["frac_of_measured_mfma_ceiling"] = round(achieved / top, 4) if top else None
         res["roofline"]["frac_of_measured_mix_ceiling"] = round(achieved / mix, 4) if mix else None
+        vmix = ceiling.get("mfma_lds_softmax_vacc", {}).get("tflops")
+        res["roofline"]["frac_of_measured_mix_ceiling_vgpr_acc"] = (
+            round(achieved / vmix, 4) if vmix else None)
     if fl:
         res["flushed"] = fl
     if with_sdpa:

@@ -127,13 +127,16 @@ def test_mfma_ceiling_probe_runs_every_mode():
     """fa2_ablate_mfma_ceiling (triton-fa2-forward_amd/ceiling.py): one short launch per mode
     completes and writes a finite value per lane; with constant operands (1.0) every lane's sum
     is exact: 16 accumulator registers x 8 MFMAs per iteration x 16 products of 1.0, per
-    accumulator, twice."""
+    accumulator, twice. The VGPR-accumulator mode (inline-asm MFMAs, hazards kept by hand) must
+    reproduce the LDS + softmax mode bit for bit: same data, same MFMAs, only the registers the
+    accumulators live in differ."""
     import ceiling
 
     lib, fn = ceiling._fn()
     wg, iters = 64, 10
     stream = torch.cuda.current_stream().cuda_stream
-    for mode in ceiling.MODES.values():
+    outs = {}
+    for name, mode in ceiling.MODES.items():
         out = torch.full((wg * 256,), float("nan"), device="cuda")
         rc = fn(mode, wg, iters, out.data_ptr(), out.numel(), stream)
         assert rc == 0, lib.fa2_ablate_last_error()
@@ -141,6 +144,8 @@ def test_mfma_ceiling_probe_runs_every_mode():
         assert torch.isfinite(out).all(), mode
         if mode == ceiling.MODES["mfma_const"]:
             assert torch.all(out == 2 * 16 * 8 * iters * 16), out[:4]
+        outs[name] = out
+    assert torch.equal(outs["mfma_lds_softmax_vacc"], outs["mfma_lds_softmax"])
 
 
 def test_hbm_read_probe_reads_every_word():

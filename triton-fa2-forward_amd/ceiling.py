@@ -18,6 +18,8 @@ amdsmi sampling the clock and the socket power:
                     exp2 per score, half a bf16 pack, half a dot2 row sum), on independent data
   mfma_exp          random, registers, one exp2 per MFMA    } what one exp2 costs beside the
   mfma_fma2         random, registers, two FMAs per MFMA    } MFMAs, against two FMAs
+  mfma_lds_softmax_vacc  mfma_lds_softmax with the accumulators in VGPRs, as the attention
+                    kernel holds them (the compiler puts the other modes' in AGPRs)
 
 Per mode: TFLOP/s, the median graphics clock and power, TFLOP/s per GHz (the issue efficiency,
 whatever the clock: the peak is 1048.6 per GHz) and the fraction of the 2.4 GHz peak.
@@ -39,7 +41,7 @@ sys.path.insert(0, HERE)
 sys.path.insert(0, os.path.dirname(HERE))
 
 MODES = {"mfma": 0, "mfma_const": 1, "mfma_lds": 2, "mfma_lds_softmax": 3,  # FA2_ABLATE_CEIL_*
-         "mfma_exp": 4, "mfma_fma2": 5}
+         "mfma_exp": 4, "mfma_fma2": 5, "mfma_lds_softmax_vacc": 6}
 PEAK_TFLOPS = 2516.6            # 256 CUs x 4096 FLOP/clk x 2.4 GHz (dense bf16/fp16)
 PEAK_MHZ = 2400.0
 MFMA_FLOP = 32 * 32 * 16 * 2    # one v_mfma_f32_32x32x16_bf16

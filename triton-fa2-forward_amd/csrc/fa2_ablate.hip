@@ -67,7 +67,7 @@ int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
 int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, float* out,
                             int64_t out_words, void* stream) {
   g_err[0] = '\0';
-  if (mode < FA2_ABLATE_CEIL_MFMA || mode > FA2_ABLATE_CEIL_MFMA_FMA2)
+  if (mode < FA2_ABLATE_CEIL_MFMA || mode > FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC)
     return fail(FA2_EINVAL, "unknown ceiling mode %d", (int)mode);
   if (workgroups < 1 || workgroups > FA2_ABLATE_CEIL_MAX_WORKGROUPS)
     return fail(FA2_EINVAL, "workgroups %d outside [1, %d]", (int)workgroups,

@@ -17,7 +17,16 @@
 //                                     half a bf16 pack, half a dot2 row sum);
 //   FA2_ABLATE_CEIL_MFMA_EXP          random operands in registers, one exp2 per MFMA;
 //   FA2_ABLATE_CEIL_MFMA_FMA2         random operands in registers, two FMAs per MFMA
-// (the last two price an exp2 against FMAs in the issue cycles beside the MFMAs).
+//   FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC  the LDS_SOFTMAX mix with the two accumulators held in
+//                                     VGPRs, where the attention kernel holds its own
+// (EXP and FMA2 price an exp2 against FMAs in the issue cycles beside the MFMAs). For every other
+// mode the compiler keeps the accumulators in AGPRs, since nothing but MFMAs touches them in the
+// loop; with vector work beside the MFMAs the two placements do not issue alike, so VACC gives
+// the mix ceiling of the kernel's own placement. Its MFMAs are inline asm in the VGPR form
+// (the compiler's own choice is one form for all of a kernel's MFMAs), and the compiler's hazard
+// recognizer does not see them: 2 wait states separate the vector writes of their operands
+// (before the loop) from the first, and the results are read once, after 12 wait states, gfx950's
+// waits around a 32x32x16 MFMA.
 // The output is meaningless; every lane writes one float so that nothing is optimised away.
 //
 // hbm_read_kernel is the memory-side counterpart (fa2_ablate_hbm_read): a streaming read of a
@@ -60,8 +69,10 @@ template <int MODE>
 __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, int iters) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr bool kRandom = MODE != FA2_ABLATE_CEIL_MFMA_CONST;
-  constexpr bool kLds = MODE == FA2_ABLATE_CEIL_MFMA_LDS || MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX;
-  constexpr bool kSoftmax = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX;
+  constexpr bool kVacc = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC;
+  constexpr bool kLds = MODE == FA2_ABLATE_CEIL_MFMA_LDS ||
+                        MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX || kVacc;
+  constexpr bool kSoftmax = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX || kVacc;
   constexpr bool kExp = MODE == FA2_ABLATE_CEIL_MFMA_EXP;
   constexpr bool kFma2 = MODE == FA2_ABLATE_CEIL_MFMA_FMA2;
   const int lane = threadIdx.x & 63;
@@ -70,7 +81,7 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
   __syncthreads();
   const char FA2_LDS* chunks = (const char FA2_LDS*)lds + lane * 16;
   const uint32_t seed = 1u << 24 | (blockIdx.x * kCeilThreads + threadIdx.x) * 4u;
-  const u32x4 b = {bf16_pair(seed, kRandom), bf16_pair(seed + 1, kRandom),
+  u32x4 b = {bf16_pair(seed, kRandom), bf16_pair(seed + 1, kRandom),
                    bf16_pair(seed + 2, kRandom), bf16_pair(seed + 3, kRandom)};
   u32x4 a[4];
 #pragma unroll
@@ -80,13 +91,21 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
   for (int j = 0; j < 8; ++j) sv[j] = (float)(mix32(seed + 8 + j) & 0xffffu) * (1.0f / 65536.0f);
   float lsum = 0.f, eprev = 0.f;
   f32x16 acc0 = {}, acc1 = {};
+  // 2 wait states between the vector writes of acc0, acc1 and b and the first asm MFMA
+  if constexpr (kVacc) asm volatile("s_nop 1" : "+v"(acc0), "+v"(acc1), "+v"(b));
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      if (i & 1)
+      if constexpr (kVacc) {
+        if (i & 1)
+          asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc1) : "v"(a[i & 3]), "v"(b));
+        else
+          asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc0) : "v"(a[i & 3]), "v"(b));
+      } else if (i & 1) {
         acc1 = Elem<1>::mma(a[i & 3], b, acc1);
-      else
+      } else {
         acc0 = Elem<1>::mma(a[i & 3], b, acc0);
+      }
       // the read for the MFMA four ahead, into the register just consumed
       if constexpr (kLds) a[i & 3] = *(const volatile u32x4 FA2_LDS*)(chunks + ((i + 4) & 15) * 1024);
       if constexpr (kSoftmax) {
@@ -102,6 +121,7 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
       }
     }
   }
+  if constexpr (kVacc) asm volatile("s_nop 7\n\ts_nop 3" : "+v"(acc0), "+v"(acc1));
   const f32x16 s = acc0 + acc1;
   float t = lsum;
   if constexpr (kExp || kFma2) {
@@ -152,6 +172,8 @@ int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStre
       return launch_ceiling<FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX>(out, workgroups, iters, s);
     case FA2_ABLATE_CEIL_MFMA_EXP:
       return launch_ceiling<FA2_ABLATE_CEIL_MFMA_EXP>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC:
+      return launch_ceiling<FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC>(out, workgroups, iters, s);
     case FA2_ABLATE_CEIL_MFMA_FMA2:
       return launch_ceiling<FA2_ABLATE_CEIL_MFMA_FMA2>(out, workgroups, iters, s);
     default: return (int)hipErrorInvalidValue;
