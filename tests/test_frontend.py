@@ -183,6 +183,10 @@ def _call(**over):
      -1, "32-bit row index"),
     (dict(h_q=8, h_kv=1, pack=8, n_q=2**28 + 1, n_kv=2**28 + 1, block_m=256),
      -1, "32-bit row index"),
+    # K/V row strides past 2^22 elements: the kernel builds a tile's buffer resource from 32-bit
+    # products of the row stride
+    (dict(sk=(1 << 40, 1 << 30, (1 << 22) + 8, 1)), -1, "sequence stride"),
+    (dict(sv=(1 << 40, 1 << 30, (1 << 22) + 8, 1)), -1, "sequence stride"),
 ])
 def test_c_abi_rejects_bad_arguments(over, code, msg):
     rc, err = _call(**over)
