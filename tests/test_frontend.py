@@ -110,6 +110,30 @@ def _declared_functions():
     return set(re.findall(r"\b(fa2_[a-z0-9_]+)\s*\(", text))
 
 
+def test_loadable_copies_only_what_the_kernel_cannot_address():
+    """fa2.kernel._loadable (CPU tensors: the check is on strides and alignment only): views the
+    16-byte loads can address pass through; a K/V row stride above the C ABI's 2^22 elements is
+    copied, one at the limit is not (the reference's attention() takes any stride)."""
+    from fa2 import kernel
+
+    base = torch.empty(1, 4, 64, 64, dtype=torch.float16)
+    assert kernel._loadable(base) is base
+    bnhd = torch.empty(1, 64, 4, 64, dtype=torch.float16).transpose(1, 2)  # [B, N, H, D] view
+    assert kernel._loadable(bnhd, kernel._MAX_KV_ROW_STRIDE) is bnhd
+    odd = torch.empty(1, 4, 64, 68, dtype=torch.float16)[..., :60]        # stride 68: not x8
+    assert kernel._loadable(odd) is not odd and kernel._loadable(odd).is_contiguous()
+    store = torch.empty(1 << 23, dtype=torch.float16)
+    at = store.as_strided((1, 1, 2, 64), (1 << 23, 1 << 23, 1 << 22, 1))
+    below = store.as_strided((1, 1, 2, 64), (1 << 23, 1 << 23, (1 << 22) - 8, 1))
+    wide = torch.empty((1 << 22) + 8 + 64, dtype=torch.float16).as_strided(
+        (1, 1, 2, 64), ((1 << 22) + 72, (1 << 22) + 72, (1 << 22) + 8, 1))
+    assert kernel._loadable(at, kernel._MAX_KV_ROW_STRIDE) is at
+    assert kernel._loadable(below, kernel._MAX_KV_ROW_STRIDE) is below
+    copied = kernel._loadable(wide, kernel._MAX_KV_ROW_STRIDE)
+    assert copied is not wide and copied.is_contiguous() and torch.equal(copied, wide)
+    assert kernel._loadable(wide) is wide   # q and out: no row-stride limit in the C ABI
+
+
 @needs_lib
 def test_library_exports_every_declared_symbol():
     declared = _declared_functions()

@@ -278,6 +278,28 @@ def test_pipelined_loop_split_kv(splits, N_kv):
 # long sequences: fp32 accumulation over hundreds of tiles, and split-KV over a long K/V
 # ------------------------------------------------------------------------------------------
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_kv_row_stride_at_the_limit(causal):
+    """K and V rows 2^22 elements apart, the largest sequence stride the C ABI takes: each K/V
+    tile's buffer resource is built from 32-bit products of it ((BN - 1) strides plus a row,
+    below 2^31 bytes). 130 keys: the last tile holds 2 rows, so its record count is clipped.
+    The views reach the kernel uncopied (fa2.kernel._loadable). Each tensor spans ~1.1 GB."""
+    from fa2 import kernel
+
+    S, n, D = 1 << 22, 130, 64
+    g = torch.Generator(device="cuda").manual_seed(130)
+    q = torch.randn(1, 2, n, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    kv = []
+    for _ in range(2):
+        store = torch.empty(n * S, device="cuda", dtype=torch.bfloat16)
+        t = store.as_strided((1, 1, n, D), (n * S, n * S, S, 1))
+        t.copy_(torch.randn(1, 1, n, D, device="cuda", dtype=torch.bfloat16, generator=g))
+        assert kernel._loadable(t, kernel._MAX_KV_ROW_STRIDE) is t
+        kv.append(t)
+    k, v = kv
+    check_against_oracle(q, k, v, causal, precision=torch.float32)
+
+
 def test_long_sequence_causal_32k():
     """bf16 causal GQA at N = 32768 (512 K/V tiles per late program), fp32 oracle per head."""
     q, k, v = make_qkv(1, 4, 1, 32768, 32768, 128, torch.bfloat16)

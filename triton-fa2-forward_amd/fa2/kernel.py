@@ -59,14 +59,21 @@ def should_pack_gqa(n_q, group, block_m):
     return _tile_efficiency(n_q, block_m) < 0.9 * _tile_efficiency(n_q * group, block_m)
 
 
-def _loadable(t):
+# K/V rows further apart than this (elements) are copied first: the C ABI takes up to 2^22, as
+# the kernel builds a K/V tile's buffer resource from 32-bit products of the row stride.
+_MAX_KV_ROW_STRIDE = 1 << 22
+
+
+def _loadable(t, max_row_stride=None):
     """t itself if the kernel's 16-byte loads can address it, else a dense copy. A contiguous
     tensor qualifies when it is 16-byte aligned: its strides are multiples of head_dim, itself a
-    multiple of 8 (the fast path, checked first: this runs four times per call)."""
+    multiple of 8 (the fast path, checked first: this runs four times per call). With
+    `max_row_stride`, a sequence stride above it also takes the copy (K and V)."""
     if t.is_contiguous() and t.data_ptr() % 16 == 0:
         return t
     ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
-          and all(n == 1 or s % 8 == 0 for n, s in zip(t.shape[:3], t.stride()[:3])))
+          and all(n == 1 or s % 8 == 0 for n, s in zip(t.shape[:3], t.stride()[:3]))
+          and (max_row_stride is None or t.shape[2] == 1 or t.stride(2) <= max_row_stride))
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
@@ -141,7 +148,8 @@ def attention(q, k, v, causal=True, sm_scale=None, block_m=None, block_n=None,
     lse = torch.empty((B, H_q, N_q), dtype=torch.float32, device=q.device) if return_lse else None
     if out.numel() == 0:
         return (out, lse) if return_lse else out
-    q_, k_, v_ = _loadable(q), _loadable(k), _loadable(v)
+    q_ = _loadable(q)
+    k_, v_ = (_loadable(t, _MAX_KV_ROW_STRIDE) for t in (k, v))
     o_ = _loadable(out)
 
     def launch():
