@@ -202,9 +202,10 @@ void attn_fwd_kernel(const Params p) {
     voff[jj] = (uint32_t)(row * p.svn + (col ^ v_key<D>(row & 15)) * 8) * 2u;
   }
   // The resource of the tile at key n0 covers its rows n0 .. min(n0 + BN, n_kv) - 1 only (the
-  // loads touch no other row). The host keeps a row stride below 2^22 elements, so its byte
-  // stride and (BN - 1) rows of it plus a row's D elements stay below 2^31: 32-bit products, the
-  // 64-bit base added once (n0 >= 0, and n0 < n_kv since only tiles of the range are issued).
+  // loads touch no other row). The host keeps a row stride at or below 2^22 elements, so its
+  // byte stride and (BN - 1) rows of it plus a row's D elements stay below 2^31: 32-bit
+  // products, the 64-bit base added once (n0 >= 0, and n0 < n_kv since only tiles of the range
+  // are issued).
   auto rsrc_at = [&](const char* base, int64_t stride, int n0) {
     const uint32_t stride2 = (uint32_t)stride * 2u;
     const uint32_t rows = (uint32_t)min(p.n_kv - n0, BN);  // 1 .. BN

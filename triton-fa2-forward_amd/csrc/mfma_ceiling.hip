@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
   const char FA2_LDS* chunks = (const char FA2_LDS*)lds + lane * 16;
   const uint32_t seed = 1u << 24 | (blockIdx.x * kCeilThreads + threadIdx.x) * 4u;
   u32x4 b = {bf16_pair(seed, kRandom), bf16_pair(seed + 1, kRandom),
-                   bf16_pair(seed + 2, kRandom), bf16_pair(seed + 3, kRandom)};
+             bf16_pair(seed + 2, kRandom), bf16_pair(seed + 3, kRandom)};
   u32x4 a[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) a[i] = *(const volatile u32x4 FA2_LDS*)(chunks + i * 1024);
@@ -97,10 +97,10 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if constexpr (kVacc) {
-        if (i & 1)
-          asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc1) : "v"(a[i & 3]), "v"(b));
-        else
-          asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc0) : "v"(a[i & 3]), "v"(b));
+        f32x16& acc = (i & 1) ? acc1 : acc0;
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                     : "+v"(acc)
+                     : "v"(a[i & 3]), "v"(b));
       } else if (i & 1) {
         acc1 = Elem<1>::mma(a[i & 3], b, acc1);
       } else {
