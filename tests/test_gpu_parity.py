@@ -278,6 +278,27 @@ def test_pipelined_loop_split_kv(splits, N_kv):
 # long sequences: fp32 accumulation over hundreds of tiles, and split-KV over a long K/V
 # ------------------------------------------------------------------------------------------
 
+@pytest.mark.parametrize("slope", [0.16, 4.0])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_running_max_grows_on_every_tile(slope, dtype, D, causal):
+    """Scores that rise along the keys: k_n = noise + slope * n * u with q . u > 0, about 12
+    (slope 0.16) or 300 (slope 4) in exp2 units per 64-key tile. Every tile of every row then
+    moves the reference max past the lazy threshold, so O and l are rescaled on every tile (the
+    path random data rarely takes); at slope 4 the rows are one-hot within the fp32 range. Both
+    loops (head_dim 64 and 128), against the oracle in fp32."""
+    B, H, N = 1, 4, 1000
+    g = torch.Generator(device="cuda").manual_seed(1000 + D)
+    q = torch.randn(B, H, N, D, device="cuda", generator=g).abs()
+    u = torch.full((D,), D ** -0.5, device="cuda")
+    ramp = slope * torch.arange(N, device="cuda", dtype=torch.float32)
+    k = torch.randn(B, H, N, D, device="cuda", generator=g) * 0.1 + ramp[:, None] * u
+    v = torch.randn(B, H, N, D, device="cuda", generator=g)
+    q, k, v = (t.to(dtype) for t in (q, k, v))
+    check_against_oracle(q, k, v, causal, precision=torch.float32)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_kv_row_stride_at_the_limit(causal):
     """K and V rows 2^22 elements apart, the largest sequence stride the C ABI takes: each K/V
