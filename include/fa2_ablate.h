@@ -33,6 +33,10 @@ extern "C" {
 #define FA2_ABLATE_NO_SOFTMAX 16       /* no mask, max, exp, sum or rescale: O = (Q K^T) V (:7)  */
 #define FA2_ABLATE_KV_L2 32            /* every K/V tile load reads the first tile again, so it
                                           hits L2 instead of HBM (:8-9)                          */
+/* Not a kernel switch and not in the reference: the launch keeps the static order of programs
+ * (workgroup b runs program b) where fa2_attn_fwd deals a causal grid's last programs at run
+ * time (its dynamic tail). Combines with any variant; the output is the same bit for bit. */
+#define FA2_ABLATE_STATIC_ORDER 128
 
 /*
  * fa2_ablate_attn_fwd - the forward kernel with the switches in `variant`.
@@ -47,6 +51,7 @@ extern "C" {
  *              FA2_ABLATE_NO_SOFTMAX                      no_softmax
  *              FA2_ABLATE_KV_L2                           kv_l2
  *              FA2_ABLATE_NO_SOFTMAX | FA2_ABLATE_KV_L2   matmul_only
+ *            each optionally with FA2_ABLATE_STATIC_ORDER;
  *            other bit sets are rejected (FA2_EINVAL).
  * The other arguments are fa2_attn_fwd's (include/fa2_fwd.h), with the same checks. Runs at the
  * default configuration (block_m 128, fa2_default_config's block_n), without split-KV, the
@@ -63,16 +68,18 @@ FA2_API int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, voi
 #define FA2_ABLATE_TIMELINE_WORDS 6
 
 /*
- * fa2_ablate_timeline - the product kernel (variant 0, same output bit for bit) with a timeline:
- * every workgroup b writes FA2_ABLATE_TIMELINE_WORDS uint64 at records[6 b ...]:
+ * fa2_ablate_timeline - the product kernel (variant 0, same output bit for bit) with a timeline,
+ * in the product's schedule (its dynamic tail included): the workgroup that runs program b (its
+ * place in the static order) writes FA2_ABLATE_TIMELINE_WORDS uint64 at records[6 b ...]:
  *   [0] entry, [1] prologue done (Q and the first K/V tiles in, first barrier passed),
  *   [2] tile loop done, [3] stores done (after a wait for them): s_memrealtime, 100 MHz;
  *   [4] the workgroup's K/V tile count;
  *   [5] XCC_ID << 32 | HW_ID (hardware ids of the wave that wrote: CU, shader array, engine).
  * It waits for its stores before the last stamp, which the product does not do. No counterpart
  * in the reference (its profiling used Nsight); a measurement tool for the schedule of short
- * grids. records: device memory, 8-byte aligned, at least 6 x workgroups words (record_words),
- * where workgroups = ceil(n_q * pack / 128) * batch * h_q / pack; else FA2_EINVAL, no launch.
+ * grids. records: device memory, 8-byte aligned, at least 6 x programs words (record_words),
+ * where programs = ceil(n_q * pack / 128) * batch * h_q / pack; else FA2_EINVAL, no launch.
+ * (The dynamic tail's spare workgroups, which find no program, write nothing.)
  */
 FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
                                 const int64_t q_stride[4], const int64_t k_stride[4],

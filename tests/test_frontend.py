@@ -445,8 +445,9 @@ def test_ablation_front_end_checks_arguments_on_the_cpu():
 
     # the reference's variant names (bench/ablation.py:42-53) and their bits
     assert list(VARIANTS) == ["copy", "scale_first", "mask_every_tile", "before_fixes", "no_exp",
-                              "no_softmax", "kv_l2", "matmul_only", "pack"]
+                              "no_softmax", "kv_l2", "matmul_only", "pack", "static_order"]
     assert variant_bits(VARIANTS["matmul_only"]) == 48
+    assert variant_bits(VARIANTS["static_order"]) == 128  # FA2_ABLATE_STATIC_ORDER, host-only
     q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
     with pytest.raises(AssertionError, match="unknown"):
         attention_ablate(q, q, q, fast=True)

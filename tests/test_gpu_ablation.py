@@ -123,6 +123,28 @@ def test_timeline_instance_is_the_product_and_its_records_are_ordered(dtype, D, 
     assert len({decode_cu(r[5]) for r in recs}) <= 256
 
 
+def test_timeline_records_every_program_once_under_the_dynamic_tail():
+    """B1 H32/8 N4096 head_dim 128 causal has a dynamic tail (1024 programs, 128 per XCD): the
+    records are indexed by program, so every program's record is written exactly once whichever
+    workgroup ran it, and the spare workgroups that found no program leave nothing."""
+    from ablation import table_free_launch
+    from timeline import run_timeline
+
+    q, k, v = make_qkv(1, 32, 8, 4096, 4096, 128, torch.bfloat16)
+    recs, out = run_timeline(q, k, v, True, 2)
+    assert torch.equal(out, table_free_launch(q, k, v, True))
+    assert sorted(r[4] for r in recs) == sorted(2 * t + 2 for t in range(32) for _ in range(32))
+    assert all(0 < r[0] <= r[1] <= r[2] <= r[3] for r in recs)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_static_order_is_copy_bit_for_bit(causal):
+    """FA2_ABLATE_STATIC_ORDER changes only which workgroup runs which program."""
+    q, k, v = make_qkv(1, 32, 8, 4096, 4096, 128, torch.bfloat16)
+    assert torch.equal(_ablate()(q, k, v, causal=causal, static_order=True),
+                       _ablate()(q, k, v, causal=causal))
+
+
 def test_mfma_ceiling_probe_runs_every_mode():
     """fa2_ablate_mfma_ceiling (triton-fa2-forward_amd/ceiling.py): one short launch per mode
     completes and writes a finite value per lane; with constant operands (1.0) every lane's sum

@@ -1,0 +1,121 @@
+"""The dynamic tail of causal grids (attn_fwd_host.hpp: tail_schedule, ticket_word).
+
+Where a causal grid has at least two rounds of programs per XCD and its (batch, kv head) units
+split evenly over the 8 XCDs, the last programs of every XCD's static order are dealt at run time:
+each workgroup past the static part takes a ticket from a per-stream word with one atomic
+increment that wraps, so the word is zero again after every launch, and a few spare workgroups
+find no program and exit. Which workgroup runs a program changes from launch to launch; what the
+program computes does not. So:
+
+* the output equals the static order's (the measurement library's FA2_ABLATE_STATIC_ORDER) bit
+  for bit, on shapes with and without GQA packing, ragged, at head_dim 64 and 128;
+* calls back to back, with tails of different sizes on one stream, keep that (every launch
+  leaves its word at zero for the next);
+* two streams running tails at the same time keep it (each stream has its own word);
+* a captured launch replays it (it holds a word of its own), with eager calls between replays.
+"""
+
+import pytest
+import torch
+
+from attn_check import make_qkv
+
+pytestmark = pytest.mark.gpu
+
+# (B, H_q, H_kv, N, D, dtype, pack): all causal, all with a tail at the default 128-row tiles
+TAIL_SHAPES = {
+    "gqa_d128": (1, 32, 8, 4096, 128, torch.bfloat16, False),   # C3's heads, 1024 programs
+    "mha_ragged": (8, 16, 16, 2000, 128, torch.bfloat16, False),  # 128 units, 16 q tiles
+    "fp16_d64": (4, 16, 16, 4096, 64, torch.float16, False),     # three workgroups per CU
+    "packed": (2, 32, 8, 2048, 128, torch.bfloat16, True),       # GQA head packing
+}
+
+
+def _static(q, k, v, pack):
+    from ablation import attention_ablate
+    return attention_ablate(q, k, v, causal=True, pack_gqa=pack, static_order=True)
+
+
+def _dynamic(q, k, v, pack, stream=None):
+    """fa2_attn_fwd at the default configuration (no key-norm table, like the variants)."""
+    import math
+
+    from fa2 import _lib
+    from fa2.kernel import LOG2E
+
+    out = torch.empty_like(q)
+    s = stream if stream is not None else torch.cuda.current_stream()
+    _lib.attn_fwd(q, k, v, out, True, q.shape[1] // k.shape[1] if pack else 1, 128, 0,
+                  LOG2E / math.sqrt(q.shape[3]), s.cuda_stream)
+    return out
+
+
+def _inputs(name, seed=0):
+    B, hq, hkv, n, d, dt, pack = TAIL_SHAPES[name]
+    return (*make_qkv(B, hq, hkv, n, n, d, dt, seed=seed), pack)
+
+
+@pytest.mark.parametrize("name", list(TAIL_SHAPES))
+def test_dynamic_tail_is_the_static_order_bit_for_bit(name):
+    q, k, v, pack = _inputs(name)
+    want = _static(q, k, v, pack)
+    for _ in range(3):
+        assert torch.equal(_dynamic(q, k, v, pack), want)
+
+
+def test_tails_of_different_sizes_back_to_back_on_one_stream():
+    """Each launch's increments bring the stream's word back to zero; a word left elsewhere would
+    shift the next launch's tickets, so that some programs ran twice and others never."""
+    cases = {name: _inputs(name, seed=3) for name in ("gqa_d128", "fp16_d64", "mha_ragged")}
+    want = {name: _static(*c) for name, c in cases.items()}
+    outs = []
+    for _ in range(2):
+        for name, c in cases.items():
+            outs.append((name, _dynamic(*c)))
+    torch.cuda.synchronize()
+    for name, out in outs:
+        assert torch.equal(out, want[name]), name
+
+
+def test_tails_on_two_streams_at_once():
+    a, b = _inputs("gqa_d128", seed=5), _inputs("mha_ragged", seed=6)
+    want_a, want_b = _static(*a), _static(*b)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            outs.append(("a", _dynamic(*a, stream=s1)))
+        with torch.cuda.stream(s2):
+            outs.append(("b", _dynamic(*b, stream=s2)))
+    torch.cuda.current_stream().wait_stream(s1)
+    torch.cuda.current_stream().wait_stream(s2)
+    torch.cuda.synchronize()
+    for which, out in outs:
+        assert torch.equal(out, want_a if which == "a" else want_b), which
+
+
+def test_captured_tail_replays_with_eager_calls_between():
+    from fa2.kernel import attention
+
+    q, k, v, _ = _inputs("gqa_d128")
+    attention(q, k, v, causal=True)             # warm up outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            captured = attention(q, k, v, causal=True)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for seed in (1, 2, 3):
+        nq, nk, nv, _ = _inputs("gqa_d128", seed=seed)
+        q.copy_(nq), k.copy_(nk), v.copy_(nv)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = attention(nq, nk, nv, causal=True)   # eager, on the current stream's word
+        torch.cuda.synchronize()
+        assert torch.equal(captured, want)

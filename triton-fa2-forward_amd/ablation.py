@@ -20,6 +20,8 @@ never loads. The reference's variants (bench/ablation.py:1-20, 42-53):
   kv_l2            every tile loads K/V tile 0 again: L2 hits instead of HBM reads
   matmul_only      no_softmax + kv_l2: the two products and the loads' issue cost
   pack             copy with GQA head packing forced on
+  static_order     copy without the dynamic tail of causal grids: workgroup b runs program b
+                   (not in the reference; what the run-time dealing of the last programs buys)
 
 Measurement (this repository's bench.py harness): the clocks are settled once (bench.settle_clocks);
 then, round after round, every variant runs W warmup launches and K launches back to back between one
@@ -50,7 +52,8 @@ sys.path.insert(0, os.path.dirname(HERE))
 ABLATE_LIB_PATH = os.path.join(HERE, "libfa2_ablate.so")
 
 # switch -> VARIANT bit (FA2_ABLATE_* in include/fa2_ablate.h)
-SWITCH_BITS = {"scale_first": 1, "mask_every_tile": 2, "no_exp": 8, "no_softmax": 16, "kv_l2": 32}
+SWITCH_BITS = {"scale_first": 1, "mask_every_tile": 2, "no_exp": 8, "no_softmax": 16, "kv_l2": 32,
+               "static_order": 128}
 KNOBS = tuple(SWITCH_BITS)
 VARIANTS = {
     "copy": (),
@@ -62,10 +65,11 @@ VARIANTS = {
     "kv_l2": ("kv_l2",),
     "matmul_only": ("no_softmax", "kv_l2"),
     "pack": ("pack",),
+    "static_order": ("static_order",),
 }
 # variants whose output must equal the product's bit for bit (the others change rounding or are
 # wrong by design)
-EXACT = ("copy", "mask_every_tile", "pack")
+EXACT = ("copy", "mask_every_tile", "pack", "static_order")
 
 _LIB = None
 

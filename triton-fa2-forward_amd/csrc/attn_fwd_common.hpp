@@ -23,9 +23,6 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 #define FA2_LDS __attribute__((address_space(3)))
 #define FA2_GLOBAL __attribute__((address_space(1)))
 
-// Compute units (8 XCDs x 32). With two workgroups per CU, the dispatcher's first round places
-// block b and block b + kCus on the same CU (measured with the hardware CU id).
-constexpr int kCus = 256;
 // Lazy-rescale threshold in exp2 units: the reference max lags the true max by at most this.
 constexpr float kRescaleTau = 8.0f;
 // Score bound from key norms: a wave whose rows all satisfy |q| |k|max qk_scale <= m + tau after

@@ -12,6 +12,9 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "attn_fwd_launch.hpp"
 #include "fa2_fwd.h"
@@ -116,6 +119,114 @@ int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim) {
   return (int32_t)chunk;
 }
 
+// Dynamic tail of causal grids. Each XCD's programs run in a static order (program_of), but the
+// XCDs do not run at one speed: their clocks differ by up to ~10% under the chip's power limit,
+// and which ones are slow changes between boxes and workloads. The last programs of every XCD's
+// order (the lightest, causal programs being taken heaviest first) are therefore dealt at run
+// time: the workgroups past static_blocks take tickets from one counter, so the XCDs that run
+// ahead take more of them, heaviest first, and a few extra workgroups (6% of the grid) give the
+// fast XCDs room for more programs than their share; the ones that find no program left exit.
+// The tail is the lighter of a quarter of each XCD's programs and half of one unit chunk (more
+// would mix the K/V of more units in each XCD's L2). Measured on MI355X against the static order
+// (back-to-back launches, same box): C3 +1.6-2.9%, C2 +1.0-1.4%, bf16 B2 H32/8 N8192 D128 causal
+// +2.3-2.7%, fp16 B4 H16 N4096 D64 causal +2.2-2.9%, B8 H16 N4096 D128 +0.7%. Non-causal grids
+// (every program the same work, so no light programs to even out the end) lost 0.3% and keep
+// the static order; so do grids of fewer than two rounds per XCD.
+struct TailSchedule {
+  int32_t static_blocks = 0, tail_wgs = 0, tail_programs = 0;  // tail_wgs == 0: static order
+};
+TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, int64_t progs_per_kv,
+                           int64_t n_tiles, int32_t chunk, int head_dim, int bn) {
+  TailSchedule s;
+  if (!causal || splits != 1 || waves != 4 || units % fa2::kXcds) return s;
+  const int64_t upx = units / fa2::kXcds;
+  const int64_t per_xcd = upx * progs_per_kv * n_tiles;
+  // workgroups one XCD holds at once: 32 CUs x (3 at head_dim 64, 64-key tiles; else 2)
+  const int64_t slots = (fa2::kCus / fa2::kXcds) * ((head_dim == 64 && bn <= 64) ? 3 : 2);
+  if (per_xcd < 2 * slots) return s;
+  const int64_t cu = (chunk > 0 && upx % chunk == 0) ? chunk : upx;  // program_of's chunk
+  const int64_t tail = std::min((per_xcd + 3) / 4, cu * progs_per_kv * n_tiles / 2);
+  const int64_t grid = per_xcd * fa2::kXcds;
+  const int64_t extra = (grid * 6 / 100 + 7) / 8 * 8;
+  if (tail < 1 || grid + extra > 0x7fffffffLL) return s;
+  s.static_blocks = (int32_t)((per_xcd - tail) * fa2::kXcds);
+  s.tail_programs = (int32_t)(tail * fa2::kXcds);
+  s.tail_wgs = (int32_t)(tail * fa2::kXcds + extra);
+  return s;
+}
+
+// The dynamic tail's ticket words: one per (device, stream), and one for every launch recorded
+// under stream capture (a graph replays its launch with the word it was recorded with, and one
+// graph's launches do not overlap). A launch's increments bring its word back to zero, the value
+// the array is loaded with, so nothing is ever cleared. Two launches that overlap in time always
+// hold different words; past kTicketWords words per device, launches run the static order.
+constexpr int kTicketWords = 1024;
+constexpr int kTicketStride = 16;  // words apart: each word on its own 64-byte line
+constexpr int kTicketDevices = 64;
+
+}  // namespace
+static __device__ __align__(256) uint32_t g_ticket_words[kTicketWords * kTicketStride] = {};
+namespace {
+
+struct TicketPool {
+  std::mutex mu;
+  uint32_t* base[kTicketDevices] = {};
+  int used[kTicketDevices] = {};
+  std::map<std::pair<int, hipStream_t>, int> by_stream;
+};
+
+TicketPool& ticket_pool() {
+  static TicketPool pool;
+  return pool;
+}
+
+// The ticket word of a launch on `stream`, or null (the launch then runs the static order): the
+// stream's device must be the current one, and the per-thread default stream gets none (its
+// handle names another stream in every thread). Runtime errors met here are cleared, so that the
+// launch after it does not report them.
+uint32_t* ticket_word(hipStream_t stream) {
+  if (stream == hipStreamPerThread) return nullptr;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kTicketDevices) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess ||
+      (cs != hipStreamCaptureStatusNone && cs != hipStreamCaptureStatusActive)) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  TicketPool& pool = ticket_pool();
+  std::lock_guard<std::mutex> lock(pool.mu);
+  if (!pool.base[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_ticket_words)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    pool.base[dev] = static_cast<uint32_t*>(p);
+  }
+  int idx = -1;
+  if (cs == hipStreamCaptureStatusNone) {
+    const auto it = pool.by_stream.find({dev, stream});
+    if (it != pool.by_stream.end()) idx = it->second;
+  }
+  if (idx < 0) {
+    if (pool.used[dev] >= kTicketWords) return nullptr;
+    idx = pool.used[dev]++;
+    if (cs == hipStreamCaptureStatusNone) pool.by_stream.emplace(std::make_pair(dev, stream), idx);
+  }
+  return pool.base[dev] + (size_t)idx * kTicketStride;
+}
+
 // Launches the attention kernel of one checked call: the product's instances in the library,
 // the timing variants (variant != 0) in the measurement library. Returns a hipError_t value.
 using KernelLaunch = int (*)(int dtype, int di, const Params& p, int waves, int block_n,
@@ -128,7 +239,8 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
                   int32_t dtype, int32_t causal, int32_t pack, int32_t block_m, int32_t block_n,
                   float qk_scale, float* lse, int32_t num_splits, void* workspace,
                   size_t workspace_bytes, int32_t variant, KernelLaunch launch_kernel,
-                  void* stream, uint64_t* timeline = nullptr, int64_t timeline_words = 0) {
+                  void* stream, uint64_t* timeline = nullptr, int64_t timeline_words = 0,
+                  bool static_order = false) {
   g_err[0] = '\0';
   // ---- shape checks (fa2/kernel.py:218-228)
   if (batch < 0 || h_q <= 0 || h_kv <= 0 || n_q < 0 || n_kv < 0)
@@ -238,6 +350,10 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   p.key_norm2 = nullptr;
   p.key_chunks = 0;
   p.timeline = nullptr;
+  p.tickets = nullptr;
+  p.static_blocks = 0;
+  p.tail_wgs = 0;
+  p.tail_programs = 0;
 
   // Split-KV: cut the key range into whole tiles; drop splits that would be empty.
   const int64_t kv_tiles = ((int64_t)n_kv + bn - 1) / bn;
@@ -263,18 +379,31 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
     if (p.part_rows * (head_dim / 4) / 256 >= 0x7fffffffLL)
       return fail(FA2_EINVAL, "split-KV merge of %lld rows is too large", (long long)p.part_rows);
   }
-  const int64_t grid = n_tiles * n_bh * splits;
+  int64_t grid = n_tiles * n_bh * splits;
   if (grid > 0x7fffffffLL)
     return fail(FA2_EINVAL, "grid of %lld workgroups is too large", (long long)grid);
-  if (timeline) {  // the measurement library's timeline variant: kTimelineWords per workgroup
+  if (timeline) {  // the measurement library's timeline variant: kTimelineWords per program
     if (timeline_words < grid * fa2::kTimelineWords)
-      return fail(FA2_EINVAL, "the timeline needs %lld words for %lld workgroups, got %lld",
+      return fail(FA2_EINVAL, "the timeline needs %lld words for %lld programs, got %lld",
                   (long long)(grid * fa2::kTimelineWords), (long long)grid,
                   (long long)timeline_words);
     p.timeline = timeline;
   }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!static_order) {
+    const TailSchedule ts = tail_schedule(causal != 0, splits, waves, n_bh / (group / pack),
+                                          group / pack, n_tiles, p.unit_chunk, head_dim, bn);
+    if (ts.tail_wgs > 0) {
+      if (uint32_t* word = ticket_word(st)) {
+        p.tickets = word;
+        p.static_blocks = ts.static_blocks;
+        p.tail_wgs = ts.tail_wgs;
+        p.tail_programs = ts.tail_programs;
+        grid = (int64_t)ts.static_blocks + ts.tail_wgs;
+      }
+    }
+  }
   // Key-norm table: used whenever the workspace has room for it beyond the split-KV partials of
   // the REQUESTED split count, fa2_workspace_bytes(..., num_splits), which is where
   // fa2_workspace_bytes_for puts it where it pays. The partials of a clamped (smaller) split

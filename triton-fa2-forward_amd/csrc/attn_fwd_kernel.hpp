@@ -93,8 +93,20 @@ void attn_fwd_kernel(const Params p) {
 
   // split-KV: consecutive workgroups are the splits of one program
   const int split = p.splits > 1 ? (int)blockIdx.x % p.splits : 0;
-  const Program pr =
-      program_of<CAUSAL>(p, p.splits > 1 ? (int)blockIdx.x / p.splits : (int)blockIdx.x);
+  int block = p.splits > 1 ? (int)blockIdx.x / p.splits : (int)blockIdx.x;
+  // dynamic tail: the workgroup's program is the next ticket, taken by one lane and passed to
+  // the others through LDS; tickets past the tail's programs have nothing to run
+  if (p.tickets != nullptr && block >= p.static_blocks) {
+    __shared__ int ticket;
+    if (tid == 0)
+      ticket = (int)__builtin_amdgcn_atomic_inc32(p.tickets, (uint32_t)(p.tail_wgs - 1),
+                                                  __ATOMIC_RELAXED, "agent");
+    __syncthreads();
+    const int t = __builtin_amdgcn_readfirstlane(ticket);
+    if (t >= p.tail_programs) return;
+    block = p.static_blocks + t;
+  }
+  const Program pr = program_of<CAUSAL>(p, block);
 
   // ---- this lane's query row: packed row r -> (position r / pack, head r % pack)
   // (fa2/kernel.py:135-139). Rows past block_m or past n_q compute on zeros and are
@@ -787,7 +799,7 @@ void attn_fwd_kernel(const Params p) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-      uint64_t* rec = p.timeline + (int64_t)blockIdx.x * kTimelineWords;
+      uint64_t* rec = p.timeline + (int64_t)block * kTimelineWords;
       rec[0] = tl_entry;
       rec[1] = tl_prologue;
       rec[2] = tl_loop;

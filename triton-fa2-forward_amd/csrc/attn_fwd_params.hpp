@@ -7,6 +7,9 @@ namespace fa2 {
 
 // Number of XCDs (each with its own L2) that the hardware deals workgroups to round-robin.
 constexpr int kXcds = 8;
+// Compute units (8 XCDs x 32). With two workgroups per CU, the dispatcher's first round places
+// block b and block b + kCus on the same CU (measured with the hardware CU id).
+constexpr int kCus = 256;
 
 // Keys per entry of the key-norm table (attn_key_norm.hip): one workgroup of the key-norm pass
 // each (C3: 1024 workgroups), and at most three entries per 128-row causal program's own rows.
@@ -52,8 +55,18 @@ struct Params {
   // more than kBoundTau (Cauchy-Schwarz) and then skips the per-tile row max.
   const float* key_norm2;  // [B * H_kv][key_chunks]
   int32_t key_chunks;      // ceil(n_kv / kKeyChunk)
-  // Measurement library only (the timeline variant): kTimelineWords uint64 per workgroup,
-  // indexed by blockIdx.x. Null, and never read, in the product's instances.
+  // Dynamic tail (causal grids; the host's tail_schedule): the workgroups from static_blocks on
+  // each take one ticket from *tickets with an agent-scope atomic increment that wraps at
+  // tail_wgs - 1, so that the word is zero again once the launch has run. Ticket t below
+  // tail_programs runs program static_blocks + t of the static order; the others exit at once.
+  // Null: workgroup b runs program b.
+  uint32_t* tickets;
+  int32_t static_blocks;
+  int32_t tail_wgs;
+  int32_t tail_programs;
+  // Measurement library only (the timeline variant): kTimelineWords uint64 per program,
+  // indexed by the program's place in the static order. Null, and never read, in the product's
+  // instances.
   uint64_t* timeline;
 };
 

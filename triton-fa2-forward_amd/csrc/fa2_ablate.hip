@@ -37,6 +37,9 @@ int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
                         int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
                         int32_t dtype, int32_t causal, int32_t pack, float qk_scale,
                         int32_t variant, void* stream) {
+  // FA2_ABLATE_STATIC_ORDER is the host's: the launch keeps the static order (no dynamic tail)
+  const bool static_order = (variant & FA2_ABLATE_STATIC_ORDER) != 0;
+  variant &= ~FA2_ABLATE_STATIC_ORDER;
   // the timeline instance writes its records: only fa2_ablate_timeline, with a buffer, runs it
   if (!fa2::ablation_variant_built(variant) || (variant & fa2::kVariantTimeline)) {
     g_err[0] = '\0';
@@ -45,7 +48,7 @@ int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
   }
   return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
                        n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
-                       nullptr, 0, variant, launch_ablate, stream);
+                       nullptr, 0, variant, launch_ablate, stream, nullptr, 0, static_order);
 }
 
 int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
