@@ -13,9 +13,9 @@
  * (a dynamic tail): their workgroups take tickets from a counter word in the library's own
  * device memory (a static array, loaded as zeros; no allocation), which every launch leaves at
  * zero again. There is one word per (device, stream), so calls on different streams and threads
- * may overlap freely, and one per launch recorded under stream capture. Launches on the
- * per-thread default stream, on a stream of another device than the current one, or past 1024
- * words per device run the static order instead. Either way the output is the same, bit for bit.
+ * may overlap freely. Launches recorded under stream capture, launches on the per-thread default
+ * stream or on a stream of another device than the current one, and launches past 1024 streams
+ * per device run the static order instead. Either way the output is the same, bit for bit.
  *
  * Return convention: 0 on success, a negative FA2_E* code on a rejected argument or a
  * failed launch; fa2_last_error() then describes the failure (thread-local string).

@@ -12,7 +12,11 @@ program computes does not. So:
 * calls back to back, with tails of different sizes on one stream, keep that (every launch
   leaves its word at zero for the next);
 * two streams running tails at the same time keep it (each stream has its own word);
-* a captured launch replays it (it holds a word of its own), with eager calls between replays.
+* a launch recorded under stream capture keeps the static order (one graph can be instantiated
+  twice and run twice at once, which would share a word): its replays equal the eager calls,
+  which use the tail, bit for bit;
+* a stream destroyed and created again (the handle comes back; hipStreamDestroy waits for the
+  stream's queued work, so the old and new streams' launches never meet on the word) keeps it.
 """
 
 import pytest
@@ -97,7 +101,7 @@ def test_tails_on_two_streams_at_once():
         assert torch.equal(out, want_a if which == "a" else want_b), which
 
 
-def test_captured_tail_replays_with_eager_calls_between():
+def test_captured_launch_keeps_the_static_order_and_replays_exactly():
     from fa2.kernel import attention
 
     q, k, v, _ = _inputs("gqa_d128")
@@ -116,6 +120,34 @@ def test_captured_tail_replays_with_eager_calls_between():
         q.copy_(nq), k.copy_(nk), v.copy_(nv)
         graph.replay()
         torch.cuda.synchronize()
-        want = attention(nq, nk, nv, causal=True)   # eager, on the current stream's word
+        want = attention(nq, nk, nv, causal=True)   # eager: the tail, on the stream's word
         torch.cuda.synchronize()
         assert torch.equal(captured, want)
+
+
+def test_a_new_stream_on_a_reused_handle_keeps_the_tail_exact():
+    """hipStreamDestroy frees the handle for the next stream created (the same address comes
+    back) once the stream's queued work has run; the new stream then starts from the word the old
+    one left at zero. Streams created and destroyed through the HIP runtime directly (torch pools
+    its own)."""
+    import ctypes
+    import math
+
+    from fa2 import _lib
+    from fa2.kernel import LOG2E
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    q, k, v, _ = _inputs("mha_ragged", seed=8)
+    want = _static(q, k, v, False)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        h = ctypes.c_void_p()
+        assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+        out = torch.empty_like(q)
+        _lib.attn_fwd(q, k, v, out, True, 1, 128, 0, LOG2E / math.sqrt(q.shape[3]), h.value)
+        assert hip.hipStreamSynchronize(h) == 0
+        assert hip.hipStreamDestroy(h) == 0
+        assert torch.equal(out, want)

@@ -155,11 +155,13 @@ TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, in
   return s;
 }
 
-// The dynamic tail's ticket words: one per (device, stream), and one for every launch recorded
-// under stream capture (a graph replays its launch with the word it was recorded with, and one
-// graph's launches do not overlap). A launch's increments bring its word back to zero, the value
-// the array is loaded with, so nothing is ever cleared. Two launches that overlap in time always
-// hold different words; past kTicketWords words per device, launches run the static order.
+// The dynamic tail's ticket words: one per (device, stream) in the library's own device memory.
+// A launch's increments bring its word back to zero, the value the array is loaded with, so
+// nothing is ever cleared, and the launches on one stream run one after another, so two launches
+// that can overlap in time never share a word. A stream's handle is reused by the next stream
+// created once it is destroyed, but hipStreamDestroy returns only when the stream's queued work
+// has run (measured: 10.6 ms for 20 queued C3 launches), so the new stream's launches cannot meet
+// the old one's. Past kTicketWords streams per device, launches run the static order.
 constexpr int kTicketWords = 1024;
 constexpr int kTicketStride = 16;  // words apart: each word on its own 64-byte line
 constexpr int kTicketDevices = 64;
@@ -180,10 +182,11 @@ TicketPool& ticket_pool() {
   return pool;
 }
 
-// The ticket word of a launch on `stream`, or null (the launch then runs the static order): the
-// stream's device must be the current one, and the per-thread default stream gets none (its
-// handle names another stream in every thread). Runtime errors met here are cleared, so that the
-// launch after it does not report them.
+// The ticket word of a launch on `stream`, or null (the launch then runs the static order). None
+// for a launch being recorded under stream capture (a graph can be instantiated twice and both
+// instances run at once, which would share the word), for the per-thread default stream (its
+// handle names another stream in every thread), or when the stream's device is not the current
+// one. Runtime errors met here are cleared, so that the launch after it does not report them.
 uint32_t* ticket_word(hipStream_t stream) {
   if (stream == hipStreamPerThread) return nullptr;
   int dev = -1;
@@ -199,8 +202,7 @@ uint32_t* ticket_word(hipStream_t stream) {
     }
   }
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess ||
-      (cs != hipStreamCaptureStatusNone && cs != hipStreamCaptureStatusActive)) {
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
     (void)hipGetLastError();
     return nullptr;
   }
@@ -214,15 +216,14 @@ uint32_t* ticket_word(hipStream_t stream) {
     }
     pool.base[dev] = static_cast<uint32_t*>(p);
   }
-  int idx = -1;
-  if (cs == hipStreamCaptureStatusNone) {
-    const auto it = pool.by_stream.find({dev, stream});
-    if (it != pool.by_stream.end()) idx = it->second;
-  }
-  if (idx < 0) {
+  int idx;
+  const auto it = pool.by_stream.find({dev, stream});
+  if (it != pool.by_stream.end()) {
+    idx = it->second;
+  } else {
     if (pool.used[dev] >= kTicketWords) return nullptr;
     idx = pool.used[dev]++;
-    if (cs == hipStreamCaptureStatusNone) pool.by_stream.emplace(std::make_pair(dev, stream), idx);
+    pool.by_stream.emplace(std::make_pair(dev, stream), idx);
   }
   return pool.base[dev] + (size_t)idx * kTicketStride;
 }
@@ -351,7 +352,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   p.key_chunks = 0;
   p.timeline = nullptr;
   p.tickets = nullptr;
-  p.static_blocks = 0;
+  p.static_blocks = 0x7fffffff;
   p.tail_wgs = 0;
   p.tail_programs = 0;
 
@@ -391,19 +392,6 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
   }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!static_order) {
-    const TailSchedule ts = tail_schedule(causal != 0, splits, waves, n_bh / (group / pack),
-                                          group / pack, n_tiles, p.unit_chunk, head_dim, bn);
-    if (ts.tail_wgs > 0) {
-      if (uint32_t* word = ticket_word(st)) {
-        p.tickets = word;
-        p.static_blocks = ts.static_blocks;
-        p.tail_wgs = ts.tail_wgs;
-        p.tail_programs = ts.tail_programs;
-        grid = (int64_t)ts.static_blocks + ts.tail_wgs;
-      }
-    }
-  }
   // Key-norm table: used whenever the workspace has room for it beyond the split-KV partials of
   // the REQUESTED split count, fa2_workspace_bytes(..., num_splits), which is where
   // fa2_workspace_bytes_for puts it where it pays. The partials of a clamped (smaller) split
@@ -430,6 +418,19 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* out,
       return fail(FA2_ELAUNCH, "key-norm launch failed: %s", hipGetErrorString((hipError_t)ke));
     p.key_norm2 = kp.out;
     p.key_chunks = kp.chunks;
+  }
+  if (!static_order) {
+    const TailSchedule ts = tail_schedule(causal != 0, splits, waves, n_bh / (group / pack),
+                                          group / pack, n_tiles, p.unit_chunk, head_dim, bn);
+    if (ts.tail_wgs > 0) {
+      if (uint32_t* word = ticket_word(st)) {
+        p.tickets = word;
+        p.static_blocks = ts.static_blocks;
+        p.tail_wgs = ts.tail_wgs;
+        p.tail_programs = ts.tail_programs;
+        grid = (int64_t)ts.static_blocks + ts.tail_wgs;
+      }
+    }
   }
   int e = launch_kernel(dtype, di, p, waves, bn, causal != 0, (unsigned)grid, st, variant);
   if (e != hipSuccess)

@@ -96,7 +96,7 @@ void attn_fwd_kernel(const Params p) {
   int block = p.splits > 1 ? (int)blockIdx.x / p.splits : (int)blockIdx.x;
   // dynamic tail: the workgroup's program is the next ticket, taken by one lane and passed to
   // the others through LDS; tickets past the tail's programs have nothing to run
-  if (p.tickets != nullptr && block >= p.static_blocks) {
+  if (block >= p.static_blocks) {
     __shared__ int ticket;
     if (tid == 0)
       ticket = (int)__builtin_amdgcn_atomic_inc32(p.tickets, (uint32_t)(p.tail_wgs - 1),

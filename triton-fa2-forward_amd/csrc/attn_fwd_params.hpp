@@ -35,6 +35,15 @@ struct Params {
   // Causal grids whose (batch, kv head) units split evenly over the XCDs: each XCD runs its
   // units unit_chunk at a time (a divisor of its unit count), q-tile-major inside a chunk.
   int32_t unit_chunk;
+  // Dynamic tail (causal grids; the host's tail_schedule): the workgroups from static_blocks on
+  // each take one ticket from *tickets with an agent-scope atomic increment that wraps at
+  // tail_wgs - 1, so that the word is zero again once the launch has run. Ticket t below
+  // tail_programs runs program static_blocks + t of the static order; the others exit at once.
+  // No tail: static_blocks = INT32_MAX (read beside the grid fields, so that the check costs the
+  // prologue no load of its own) and workgroup b runs program b.
+  int32_t static_blocks;
+  int32_t tail_wgs;
+  int32_t tail_programs;
   float qk_scale;   // sm_scale * log2(e)
   // Optional outputs beyond the reference's:
   float* lse;        // [B, H_q, N_q] natural-log log-sum-exp of the scaled scores, or null;
@@ -55,15 +64,7 @@ struct Params {
   // more than kBoundTau (Cauchy-Schwarz) and then skips the per-tile row max.
   const float* key_norm2;  // [B * H_kv][key_chunks]
   int32_t key_chunks;      // ceil(n_kv / kKeyChunk)
-  // Dynamic tail (causal grids; the host's tail_schedule): the workgroups from static_blocks on
-  // each take one ticket from *tickets with an agent-scope atomic increment that wraps at
-  // tail_wgs - 1, so that the word is zero again once the launch has run. Ticket t below
-  // tail_programs runs program static_blocks + t of the static order; the others exit at once.
-  // Null: workgroup b runs program b.
-  uint32_t* tickets;
-  int32_t static_blocks;
-  int32_t tail_wgs;
-  int32_t tail_programs;
+  uint32_t* tickets;  // the tail's ticket word (read only past static_blocks)
   // Measurement library only (the timeline variant): kTimelineWords uint64 per program,
   // indexed by the program's place in the static order. Null, and never read, in the product's
   // instances.
