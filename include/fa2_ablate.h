@@ -126,6 +126,20 @@ FA2_API int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t it
 FA2_API int fa2_ablate_hbm_read(const void* src, int64_t bytes, uint32_t* out, int64_t out_words,
                                 int32_t workgroups, void* stream);
 
+/*
+ * fa2_ablate_tail_schedule - the dynamic tail fa2_attn_fwd gives a launch at the default
+ * configuration (block_m 128, the default block_n, no split-KV): of its programs, the first
+ * *static_blocks run in the static order and the last *tail_programs are dealt at run time to
+ * *tail_workgroups workgroups (the spare ones find no program). All three are 0 when the launch
+ * keeps the static order (non-causal, fewer than two rounds of programs per XCD, or units that
+ * do not split evenly over the XCDs). Host-side policy only, no GPU call. FA2_EINVAL for sizes
+ * attention would reject (h_q % h_kv, head_dim, pack not 1 or the group).
+ */
+FA2_API int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                                     int32_t head_dim, int32_t causal, int32_t pack,
+                                     int32_t* static_blocks, int32_t* tail_programs,
+                                     int32_t* tail_workgroups);
+
 /* Thread-local description of this library's last failure in this thread ("" if none). */
 FA2_API const char* fa2_ablate_last_error(void);
 

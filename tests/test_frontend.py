@@ -359,11 +359,51 @@ def test_product_library_exports_its_api_and_no_timing_variant():
 
 
 @needs_ablate
+def test_dynamic_tail_policy_on_the_cpu():
+    """fa2_ablate_tail_schedule: which launches deal their last programs at run time, and how many
+    (attn_fwd_host.hpp: tail_schedule). Causal grids of whole (batch, kv head) units per XCD and at
+    least two rounds of programs per XCD (64 slots at head_dim 128, 96 at 64): the tail is the
+    lighter of a quarter of each XCD's programs and half a unit chunk, plus 6% spare workgroups
+    (rounded up to a multiple of 8). Known answers worked by hand from those rules."""
+    from ablation import ablate_lib
+
+    lib = ablate_lib()
+    fn = lib.fa2_ablate_tail_schedule
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int32] * 7 + [ctypes.POINTER(ctypes.c_int32)] * 3
+
+    def tail(B, hq, hkv, n, d, causal, pack=1):
+        out = [ctypes.c_int32(-1) for _ in range(3)]
+        rc = fn(B, hq, hkv, n, d, int(causal), pack, *(ctypes.byref(o) for o in out))
+        return rc, tuple(o.value for o in out)
+
+    # C3: 2048 programs, 256 per XCD, chunk of one unit (256 programs): a quarter, 64 per XCD
+    assert tail(1, 32, 8, 8192, 128, True) == (0, (1536, 512, 640))
+    # C2: 8 units per XCD in chunks of 4 (2 MiB units): half a chunk = a quarter = 64
+    assert tail(4, 16, 16, 4096, 128, True) == (0, (1536, 512, 640))
+    # B8 H16 N4096: 512 per XCD; half a chunk (64) is lighter than a quarter (128)
+    assert tail(8, 16, 16, 4096, 128, True) == (0, (3584, 512, 760))
+    # fp16 head_dim 64 (three workgroups per CU): 256 per XCD >= 2 x 96
+    assert tail(4, 16, 16, 4096, 64, True) == (0, (1536, 512, 640))
+    # GQA head packing: 1024 programs, 128 per XCD, a quarter = 32
+    assert tail(2, 32, 8, 2048, 128, True, pack=4) == (0, (768, 256, 320))
+    # static order: non-causal (C4), units that do not split over 8 XCDs (C5), under two rounds
+    assert tail(2, 16, 16, 16384, 64, False) == (0, (0, 0, 0))
+    assert tail(3, 28, 4, 1000, 128, True) == (0, (0, 0, 0))
+    assert tail(1, 32, 8, 2048, 128, True) == (0, (0, 0, 0))
+    assert tail(2, 16, 16, 4096, 64, True) == (0, (0, 0, 0))   # 128 per XCD < 2 x 96
+    # sizes attention() rejects
+    for bad in ((1, 30, 8, 512, 128, True), (1, 32, 8, 512, 48, True), (1, 32, 8, 512, 128, True, 3)):
+        rc, _ = tail(*bad)
+        assert rc == -1 and lib.fa2_ablate_last_error(), bad
+
+
+@needs_ablate
 def test_measurement_library_exports_exactly_its_header():
     names = _exported(ABLATE_LIB)
     assert {n for n in names if n.startswith("fa2_")} == _c_names(ABLATE_HEADER) == {
         "fa2_ablate_attn_fwd", "fa2_ablate_timeline", "fa2_ablate_mfma_ceiling",
-        "fa2_ablate_hbm_read", "fa2_ablate_last_error"}
+        "fa2_ablate_hbm_read", "fa2_ablate_tail_schedule", "fa2_ablate_last_error"}
     # the knockouts are compiled into it: kernel instances with the no_exp, no_softmax and
     # kv_l2 bits, and matmul_only (no_softmax | kv_l2); and the timeline instance (64)
     variants = {int(m.group(1)) for n in names for m in [re.search(r"ELb[01]ELi(\d+)EEEv", n)] if m}

@@ -67,6 +67,35 @@ int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
                        record_words);
 }
 
+int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                             int32_t head_dim, int32_t causal, int32_t pack,
+                             int32_t* static_blocks, int32_t* tail_programs,
+                             int32_t* tail_workgroups) {
+  g_err[0] = '\0';
+  if (!static_blocks || !tail_programs || !tail_workgroups) return fail(FA2_EINVAL, "null output");
+  *static_blocks = *tail_programs = *tail_workgroups = 0;
+  if (batch < 1 || h_q < 1 || h_kv < 1 || n_q < 1 || h_q % h_kv)
+    return fail(FA2_EINVAL, "bad sizes: batch=%d h_q=%d h_kv=%d n_q=%d", batch, h_q, h_kv, n_q);
+  if (dim_index(head_dim) < 0)
+    return fail(FA2_EINVAL, "head_dim must be a power of two in [16, 128], got %d", head_dim);
+  const int group = h_q / h_kv;
+  if (pack != 1 && pack != group)
+    return fail(FA2_EINVAL, "pack must be 1 or the GQA group %d, got %d", group, pack);
+  if (128 % pack)
+    return fail(FA2_EINVAL, "pack_gqa needs BLOCK_M (128) to be a multiple of the group (%d)", pack);
+  // attn_fwd_impl's grid at block_m 128 (4 waves) and the default K/V tile
+  const int64_t n_tiles = ((int64_t)n_q * pack + 127) / 128;
+  const int64_t n_bh = (int64_t)batch * (h_q / pack);
+  const int64_t units = n_bh / (group / pack);
+  const TailSchedule ts =
+      tail_schedule(causal != 0, 1, 4, units, group / pack, n_tiles,
+                    unit_chunk(units, n_q, head_dim), head_dim, tile_n(0, head_dim));
+  *static_blocks = ts.static_blocks;
+  *tail_programs = ts.tail_programs;
+  *tail_workgroups = ts.tail_wgs;
+  return 0;
+}
+
 int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, float* out,
                             int64_t out_words, void* stream) {
   g_err[0] = '\0';
