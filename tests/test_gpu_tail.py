@@ -151,3 +151,21 @@ def test_a_new_stream_on_a_reused_handle_keeps_the_tail_exact():
         assert hip.hipStreamSynchronize(h) == 0
         assert hip.hipStreamDestroy(h) == 0
         assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("block_n", [32, 64, 128])
+def test_tail_with_lse_and_other_tiles(block_n):
+    """The tail with the log-sum-exp output and with 32-, 64- and 128-key tiles (the policy holds
+    at every tile width of the 128-row programs): the output within the 2x-SDPA rule of the fp32
+    oracle, the same bits as the call without the log-sum-exp, and the log-sum-exp within 1e-4 of
+    the oracle's."""
+    from attn_check import check_against_oracle
+    from fa2.kernel import attention
+    from oracle import reference as ref
+
+    q, k, v, _ = _inputs("gqa_d128", seed=11)
+    out, lse = attention(q, k, v, causal=True, block_n=block_n, return_lse=True)
+    assert torch.equal(out, attention(q, k, v, causal=True, block_n=block_n))
+    check_against_oracle(q, k, v, True, precision=torch.float32, ours=out)
+    want = ref.naive_lse(q.float(), k.float(), None, causal=True)
+    assert (lse - want).abs().max().item() <= 1e-4
