@@ -169,3 +169,17 @@ def test_tail_with_lse_and_other_tiles(block_n):
     check_against_oracle(q, k, v, True, precision=torch.float32, ours=out)
     want = ref.naive_lse(q.float(), k.float(), None, causal=True)
     assert (lse - want).abs().max().item() <= 1e-4
+
+
+def test_tail_with_a_ragged_pack_of_seven():
+    """GQA group 7 at block_m 112 (C5's group on a grid long enough for a tail): packed and
+    unpacked launches both deal their tails at run time, stay equal bit for bit (packing only
+    renumbers rows) and meet the oracle."""
+    from attn_check import check_against_oracle
+    from fa2.kernel import attention
+
+    q, k, v = make_qkv(2, 56, 8, 2048, 2048, 128, torch.bfloat16, seed=12)
+    packed = attention(q, k, v, causal=True, block_m=112, pack_gqa=True)
+    unpacked = attention(q, k, v, causal=True, block_m=112, pack_gqa=False)
+    assert torch.equal(packed, unpacked)
+    check_against_oracle(q, k, v, True, precision=torch.float32, ours=packed)
