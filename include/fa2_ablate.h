@@ -131,8 +131,8 @@ FA2_API int fa2_ablate_hbm_read(const void* src, int64_t bytes, uint32_t* out, i
  * configuration (block_m 128, the default block_n, no split-KV): of its programs, the first
  * *static_blocks run in the static order and the last *tail_programs are dealt at run time to
  * *tail_workgroups workgroups (the spare ones find no program). All three are 0 when the launch
- * keeps the static order (non-causal, fewer than two rounds of programs per XCD, or units that
- * do not split evenly over the XCDs). Host-side policy only, no GPU call. FA2_EINVAL for sizes
+ * keeps the static order (non-causal, or fewer than two rounds of programs per XCD). Host-side
+ * policy only, no GPU call. FA2_EINVAL for sizes
  * attention would reject (h_q % h_kv, head_dim, pack not 1 or the group).
  */
 FA2_API int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,

@@ -361,10 +361,11 @@ def test_product_library_exports_its_api_and_no_timing_variant():
 @needs_ablate
 def test_dynamic_tail_policy_on_the_cpu():
     """fa2_ablate_tail_schedule: which launches deal their last programs at run time, and how many
-    (attn_fwd_host.hpp: tail_schedule). Causal grids of whole (batch, kv head) units per XCD and at
-    least two rounds of programs per XCD (64 slots at head_dim 128, 96 at 64): the tail is the
-    lighter of a quarter of each XCD's programs and half a unit chunk, plus 6% spare workgroups
-    (rounded up to a multiple of 8). Known answers worked by hand from those rules."""
+    (attn_fwd_host.hpp: tail_schedule). Causal grids of at least two rounds of programs per XCD
+    (64 slots at head_dim 128, 96 at 64): with whole (batch, kv head) units per XCD the tail is the
+    lighter of a quarter of each XCD's programs and half a unit chunk; otherwise (the fallback
+    order) a quarter of every XCD's blocks and the remainder; plus 6% spare workgroups (rounded up
+    to a multiple of 8). Known answers worked by hand from those rules."""
     from ablation import ablate_lib
 
     lib = ablate_lib()
@@ -387,7 +388,11 @@ def test_dynamic_tail_policy_on_the_cpu():
     assert tail(4, 16, 16, 4096, 64, True) == (0, (1536, 512, 640))
     # GQA head packing: 1024 programs, 128 per XCD, a quarter = 32
     assert tail(2, 32, 8, 2048, 128, True, pack=4) == (0, (768, 256, 320))
-    # static order: non-causal (C4), units that do not split over 8 XCDs (C5), under two rounds
+    # the fallback order (12 units): 2688 programs, 336 per XCD, a quarter = 84 per XCD
+    assert tail(3, 28, 4, 4096, 128, True) == (0, (2016, 672, 840))
+    # ... with a remainder: B1 H20/4 N8192, 1280 programs, 160 per XCD -> 40; 20 units: 5 x 256
+    assert tail(1, 20, 4, 8192, 128, True) == (0, (960, 320, 400))
+    # static order: non-causal (C4), fewer than two rounds (C5: 672 programs), under two rounds
     assert tail(2, 16, 16, 16384, 64, False) == (0, (0, 0, 0))
     assert tail(3, 28, 4, 1000, 128, True) == (0, (0, 0, 0))
     assert tail(1, 32, 8, 2048, 128, True) == (0, (0, 0, 0))

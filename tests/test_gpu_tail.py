@@ -1,7 +1,8 @@
 """The dynamic tail of causal grids (attn_fwd_host.hpp: tail_schedule, ticket_word).
 
-Where a causal grid has at least two rounds of programs per XCD and its (batch, kv head) units
-split evenly over the 8 XCDs, the last programs of every XCD's static order are dealt at run time:
+Where a causal grid has at least two rounds of programs per XCD, the last programs of every XCD's
+static order (program_of's XCD order, or its fallback order where the (batch, kv head) units do
+not split evenly over the 8 XCDs) are dealt at run time:
 each workgroup past the static part takes a ticket from a per-stream word with one atomic
 increment that wraps, so the word is zero again after every launch, and a few spare workgroups
 find no program and exit. Which workgroup runs a program changes from launch to launch; what the
@@ -32,6 +33,7 @@ TAIL_SHAPES = {
     "mha_ragged": (8, 16, 16, 2000, 128, torch.bfloat16, False),  # 128 units, 16 q tiles
     "fp16_d64": (4, 16, 16, 4096, 64, torch.float16, False),     # three workgroups per CU
     "packed": (2, 32, 8, 2048, 128, torch.bfloat16, True),       # GQA head packing
+    "fallback": (3, 28, 4, 4096, 128, torch.bfloat16, False),    # 12 units: the fallback order
 }
 
 

@@ -129,26 +129,40 @@ int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim) {
 // The tail is the lighter of a quarter of each XCD's programs and half of one unit chunk (more
 // would mix the K/V of more units in each XCD's L2). Measured on MI355X against the static order
 // (back-to-back launches, same box): C3 +1.6-2.9%, C2 +1.0-1.4%, bf16 B2 H32/8 N8192 D128 causal
-// +2.3-2.7%, fp16 B4 H16 N4096 D64 causal +2.2-2.9%, B8 H16 N4096 D128 +0.7%. Non-causal grids
-// (every program the same work, so no light programs to even out the end) lost 0.3% and keep
-// the static order; so do grids of fewer than two rounds per XCD.
+// +2.3-2.7%, fp16 B4 H16 N4096 D64 causal +2.2-2.9%, B8 H16 N4096 D128 +0.7%; grids whose units
+// do not split over the XCDs (program_of's fallback order; a quarter of every XCD's blocks):
+// B3 H28/4 N4096 +1.2%, N8192 +1.9%, B1 H20/4 N8192 +2.7%. Non-causal grids (every program the
+// same work, so no light programs to even out the end) lost 0.3% and keep the static order; so
+// do grids of fewer than two rounds per XCD.
 struct TailSchedule {
   int32_t static_blocks = 0, tail_wgs = 0, tail_programs = 0;  // tail_wgs == 0: static order
 };
 TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, int64_t progs_per_kv,
                            int64_t n_tiles, int32_t chunk, int head_dim, int bn) {
   TailSchedule s;
-  if (!causal || splits != 1 || waves != 4 || units % fa2::kXcds) return s;
-  const int64_t upx = units / fa2::kXcds;
-  const int64_t per_xcd = upx * progs_per_kv * n_tiles;
+  if (!causal || splits != 1 || waves != 4) return s;
   // workgroups one XCD holds at once: 32 CUs x (3 at head_dim 64, 64-key tiles; else 2)
   const int64_t slots = (fa2::kCus / fa2::kXcds) * ((head_dim == 64 && bn <= 64) ? 3 : 2);
+  const int64_t grid = units * progs_per_kv * n_tiles;
+  const int64_t extra = (grid * 6 / 100 + 7) / 8 * 8;
+  if (grid + extra > 0x7fffffffLL) return s;
+  if (units % fa2::kXcds) {
+    // program_of's fallback order (q tile outermost, heaviest first; the hardware still deals
+    // block b to XCD b % 8): the last quarter of every XCD's blocks, and the remainder
+    const int64_t per_xcd = grid / fa2::kXcds;
+    if (per_xcd < 2 * slots) return s;
+    const int64_t static_blocks = (per_xcd - (per_xcd + 3) / 4) * fa2::kXcds;
+    s.static_blocks = (int32_t)static_blocks;
+    s.tail_programs = (int32_t)(grid - static_blocks);
+    s.tail_wgs = (int32_t)(grid - static_blocks + extra);
+    return s;
+  }
+  const int64_t upx = units / fa2::kXcds;
+  const int64_t per_xcd = upx * progs_per_kv * n_tiles;
   if (per_xcd < 2 * slots) return s;
   const int64_t cu = (chunk > 0 && upx % chunk == 0) ? chunk : upx;  // program_of's chunk
   const int64_t tail = std::min((per_xcd + 3) / 4, cu * progs_per_kv * n_tiles / 2);
-  const int64_t grid = per_xcd * fa2::kXcds;
-  const int64_t extra = (grid * 6 / 100 + 7) / 8 * 8;
-  if (tail < 1 || grid + extra > 0x7fffffffLL) return s;
+  if (tail < 1) return s;
   s.static_blocks = (int32_t)((per_xcd - tail) * fa2::kXcds);
   s.tail_programs = (int32_t)(tail * fa2::kXcds);
   s.tail_wgs = (int32_t)(tail * fa2::kXcds + extra);
