@@ -185,3 +185,35 @@ def test_tail_with_a_ragged_pack_of_seven():
     unpacked = attention(q, k, v, causal=True, block_m=112, pack_gqa=False)
     assert torch.equal(packed, unpacked)
     check_against_oracle(q, k, v, True, precision=torch.float32, ours=packed)
+
+
+def test_seeded_random_tail_shapes_are_the_static_order_bit_for_bit():
+    """Eight seeded random causal shapes that the policy gives a tail (fa2_ablate_tail_schedule
+    says so before the launch): batch 1-6, 1-8 kv heads, GQA groups 1-8, N 1500-6000 (ragged last
+    q tiles), head_dim 64 or 128, fp16 or bf16, packed or not where the group divides 128."""
+    import ctypes
+    import random
+
+    from ablation import ablate_lib
+
+    lib = ablate_lib()
+    fn = lib.fa2_ablate_tail_schedule
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int32] * 7 + [ctypes.POINTER(ctypes.c_int32)] * 3
+    rng = random.Random(2026)
+    done = 0
+    while done < 8:
+        B, hkv, group = rng.randint(1, 6), rng.randint(1, 8), rng.choice([1, 2, 4, 7, 8])
+        n, d = rng.randint(1500, 6000), rng.choice([64, 128])
+        dt = rng.choice([torch.float16, torch.bfloat16])
+        pack = group > 1 and 128 % group == 0 and rng.random() < 0.5
+        if B * hkv * group * n * d > 6e7:  # keep each case to a few hundred MB at most
+            continue
+        out = [ctypes.c_int32() for _ in range(3)]
+        rc = fn(B, hkv * group, hkv, n, d, 1, group if pack else 1, *(ctypes.byref(o) for o in out))
+        if rc != 0 or out[1].value == 0:
+            continue
+        q, k, v = make_qkv(B, hkv * group, hkv, n, n, d, dt, seed=done)
+        want = _static(q, k, v, pack)
+        assert torch.equal(_dynamic(q, k, v, pack), want), (B, hkv, group, n, d, dt, pack)
+        done += 1
