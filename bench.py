@@ -445,6 +445,29 @@ def sustained_clock(fn, seconds=1.0):
     return out
 
 
+def tail_schedule_info(B, H_q, H_kv, N, D, causal):
+    """The dynamic tail the library gives this launch (fa2_ablate_tail_schedule, a host-side
+    policy query in the measurement library): programs run in the static order, programs dealt
+    at run time and the workgroups that take them; None where the launch keeps the static order
+    or the measurement library is not built."""
+    import ctypes
+
+    import ablation
+
+    try:
+        lib = ablation.ablate_lib()
+    except RuntimeError:
+        return None
+    fn = lib.fa2_ablate_tail_schedule
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int32] * 7 + [ctypes.POINTER(ctypes.c_int32)] * 3
+    out = [ctypes.c_int32() for _ in range(3)]
+    if fn(B, H_q, H_kv, N, D, int(causal), 1, *(ctypes.byref(o) for o in out)) != 0 or not out[1].value:
+        return None
+    return {"static_programs": out[0].value, "tail_programs": out[1].value,
+            "tail_workgroups": out[2].value}
+
+
 def measured_ceiling(seconds=1.0):
     """The MFMA rate this box sustains under its power limit (triton-fa2-forward_amd/ceiling.py,
     fa2_ablate_mfma_ceiling in the measurement library): bf16 MFMAs on random operands alone, and
@@ -528,6 +551,7 @@ def run(name, steps, warmup, with_cpu, flush_iters, with_sdpa=False, ceiling=Non
         "config": {"workload": describe(name), "batch": B, "h_q": H_q, "h_kv": k.shape[1],
                    "seq_len": N, "head_dim": D, "causal": causal, "flops_per_step": flops,
                    "flops_rule": "4*B*H_q*pairs*D, causal pairs N(N+1)/2 (bench/bench.py:83-87)"},
+        "dynamic_tail": tail_schedule_info(B, H_q, k.shape[1], N, D, causal),
         "pct_of_peak": round(100 * value / PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(PEAK_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
