@@ -4,6 +4,11 @@
     python bench.py [--steps K] [--warmup W] [--config C3] [--all] [--no-cpu-baseline]
     python bench.py --pack-short     # the reference's few-queries table (K/V read rate)
     python bench.py --all --sdpa     # also torch's own fused SDPA on the same inputs, for context
+    python bench.py --seqlens 1024 4096 16384 --dtype bf16 [--batch --hq --hkv --head-dim
+                    --kv-len --no-causal --iters --no-flush --providers --out]
+                                     # the reference's sweep (bench/bench.py:226-307): a table of
+                                     # median TFLOP/s per N and provider (fa2, fa2-nopack,
+                                     # fa2-pack, sdpa), instead of the JSON line
 
 Workload: BASELINE.json's target config C3 (bf16 causal GQA, B=1, H_q=32, H_kv=8, N=8192,
 D=128), the shape the reference's own bench defaults to (bench/bench.py:228-235) and the one
@@ -648,6 +653,111 @@ def run_pack_short(n_q, steps, warmup):
     }
 
 
+SWEEP_PROVIDERS = ("fa2", "fa2-nopack", "fa2-pack", "sdpa")
+
+
+def sweep_provider(name, q, k, v, causal):
+    """A zero-argument launch of `name` on (q, k, v), or None where it does not apply: fa2 is
+    attention() with its own packing choice, fa2-nopack / fa2-pack force the GQA layout, sdpa is
+    torch's fused SDPA (flash, else memory-efficient) on K/V expanded to MHA beforehand."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from fa2.kernel import attention
+
+    if name.startswith("fa2"):
+        pack = {"fa2": None, "fa2-nopack": False, "fa2-pack": True}[name]
+        return lambda: attention(q, k, v, causal=causal, pack_gqa=pack)
+    group = q.shape[1] // k.shape[1]
+    ke = k.repeat_interleave(group, dim=1).contiguous()
+    ve = v.repeat_interleave(group, dim=1).contiguous()
+    for backend in ("FLASH_ATTENTION", "EFFICIENT_ATTENTION"):
+        def fn(backend=backend):
+            with sdpa_kernel(getattr(SDPBackend, backend)):
+                return F.scaled_dot_product_attention(q, ke, ve, is_causal=causal)
+        try:
+            fn()
+            return fn
+        except RuntimeError:
+            continue
+    return None
+
+
+def run_seqlens(args):
+    """The reference's sweep (bench/bench.py:226-307) on this GPU: for every N and provider, the
+    correctness gate (max-abs vs SDPA <= 2e-2), then per-launch HIP events over --iters launches
+    after --warmup, each after a 1 GiB flush unless --no-flush; median TFLOP/s and IQR. Prints a
+    line per (N, provider) and the Markdown table; writes the rows as JSON to --out if given.
+    One difference from the reference's loop: each provider first runs back to back for 0.3 s
+    (settle_clocks), so that the first provider of every N is not timed on clocks still ramping
+    up from idle (without it the first provider ran up to 4% slower than the same call later)."""
+    import torch
+
+    causal = not args.no_causal
+    if causal and args.kv_len:
+        raise SystemExit("--kv-len needs --no-causal (causal here assumes N_q == N_kv)")
+    dtype = {"fp16": torch.float16, "bf16": torch.bfloat16}[args.dtype]
+    env = gpu_env()
+    rows = []
+    for n in args.seqlens:
+        n_kv = args.kv_len or n
+        g = torch.Generator(device="cuda").manual_seed(0)
+        q = torch.randn(args.batch, args.hq, n, args.head_dim, device="cuda", dtype=dtype, generator=g)
+        k = torch.randn(args.batch, args.hkv, n_kv, args.head_dim, device="cuda", dtype=dtype, generator=g)
+        v = torch.randn(args.batch, args.hkv, n_kv, args.head_dim, device="cuda", dtype=dtype, generator=g)
+        flops = attn_flops(args.batch, args.hq, n, n_kv, args.head_dim, causal)
+        kv_bytes = 2 * k.numel() * k.element_size()
+        for name in args.providers:
+            try:
+                fn = sweep_provider(name, q, k, v, causal)
+                if fn is None:
+                    raise RuntimeError("no fused SDPA backend for this shape")
+                err, _ = correctness_gate(fn(), q, k, v, causal)
+                if err is None or not math.isfinite(err) or err > 2e-2:
+                    raise RuntimeError(f"output vs SDPA: max-abs {err}")
+                settle_clocks(fn, min_ms=300.0)
+                for _ in range(args.warmup):
+                    fn()
+                torch.cuda.synchronize()
+                if args.no_flush:
+                    ms = time_each(fn, args.iters)
+                    q1, med, q3 = statistics.quantiles(ms, n=4, method="inclusive")
+                    st = {"median_ms": med, "p25_ms": q1, "p75_ms": q3}
+                else:
+                    st = flushed_median(fn, args.iters)
+            except (RuntimeError, ValueError) as e:  # a provider that does not apply is skipped
+                print(f"  skip {name:11s} N={n:6d}: {type(e).__name__}: {str(e)[:120]}", flush=True)
+                continue
+            row = {"provider": name, "seqlen": n, "kv_len": n_kv, "max_abs_err_vs_sdpa": err,
+                   "median_ms": round(st["median_ms"], 5), "p25_ms": round(st["p25_ms"], 5),
+                   "p75_ms": round(st["p75_ms"], 5),
+                   "iqr_ms": round(st["p75_ms"] - st["p25_ms"], 5),
+                   "tflops": round(flops / (st["median_ms"] * 1e-3) / 1e12, 2),
+                   "kv_tbps": round(kv_bytes / (st["median_ms"] * 1e-3) / 1e12, 3)}
+            rows.append(row)
+            print(f"  {name:11s} N={n:6d}  {row['median_ms']:8.3f} ms [IQR {row['p25_ms']:.3f}-"
+                  f"{row['p75_ms']:.3f}]  {row['tflops']:7.1f} TFLOP/s  K/V {row['kv_tbps']:5.2f} TB/s",
+                  flush=True)
+        del q, k, v
+        torch.cuda.empty_cache()
+    names = [p for p in args.providers if any(r["provider"] == p for r in rows)]
+    kv = f" N_kv={args.kv_len}" if args.kv_len else ""
+    print(f"\nB={args.batch} H_q={args.hq} H_kv={args.hkv} D={args.head_dim}{kv} {args.dtype} "
+          f"causal={causal} {'' if args.no_flush else 'flushed '}| median TFLOP/s (IQR ms)\n")
+    print("| N | " + " | ".join(names) + " |")
+    print("|---|" + "---|" * len(names))
+    for n in args.seqlens:
+        cells = []
+        for p in names:
+            r = next((r for r in rows if r["provider"] == p and r["seqlen"] == n), None)
+            cells.append(f"{r['tflops']:.1f} ({r['iqr_ms']:.3f})" if r else "-")
+        print(f"| {n} | " + " | ".join(cells) + " |")
+    if args.out:
+        with open(args.out, "w") as f:
+            json.dump({"env": env, "config": vars(args), "results": rows}, f, indent=1)
+        print(f"\nwrote {args.out}")
+
+
 def main():
     ap = argparse.ArgumentParser(description="MI355X FlashAttention-2 forward benchmark")
     ap.add_argument("--gpus", type=int, default=1)
@@ -664,6 +774,21 @@ def main():
                          "--pack-short fa2_ablate_hbm_read, ~5 s)")
     ap.add_argument("--sdpa", action="store_true",
                     help="also time torch's fused SDPA on the same inputs (sdpa_same_box, context)")
+    sw = ap.add_argument_group("the reference's sequence-length sweep (bench/bench.py:226-307)")
+    sw.add_argument("--seqlens", type=int, nargs="+", default=None,
+                    help="N_q values (also N_kv unless --kv-len): print the sweep table instead")
+    sw.add_argument("--kv-len", type=int, default=None, help="fixed N_kv (non-causal only)")
+    sw.add_argument("--batch", type=int, default=1)
+    sw.add_argument("--hq", type=int, default=32)
+    sw.add_argument("--hkv", type=int, default=8)
+    sw.add_argument("--head-dim", type=int, default=128)
+    sw.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
+    sw.add_argument("--no-causal", action="store_true")
+    sw.add_argument("--iters", type=int, default=20)
+    sw.add_argument("--no-flush", action="store_true")
+    sw.add_argument("--providers", nargs="+", default=list(SWEEP_PROVIDERS[:1]) + ["sdpa"],
+                    choices=list(SWEEP_PROVIDERS))
+    sw.add_argument("--out", default=None, help="also write the rows as JSON here")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -677,6 +802,9 @@ def main():
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs the GPU")
+    if args.seqlens:
+        run_seqlens(args)
+        return
     if args.pack_short:
         hbm = None
         if not args.no_ceiling:
