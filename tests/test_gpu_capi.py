@@ -30,6 +30,7 @@ CASES = [
     (2, 8, 2, 77, 1000, 64, 0, False, 4, 128, 0, 0, True),       # packed, split-KV, log-sum-exp
     (1, 4, 4, 129, 129, 32, 0, True, 1, 64, 32, 1, True),        # non-default tiles
     (3, 28, 4, 1000, 1000, 128, 1, True, 7, 112, 0, 1, False),   # C5's shape, packed
+    (1, 32, 8, 4096, 4096, 128, 0, True, 1, 128, 0, 1, False),   # a dynamic tail (1024 programs)
 ]
 
 
