@@ -3,7 +3,9 @@ through the C ABI, its output must equal fa2_attn_fwd_ex's bit for bit when fa2_
 a workspace of fa2_workspace_bytes_for(...) bytes. The checks use two calls in a row on the
 library's shared scratch, the second with a smaller input, so the first call's leftovers in the
 scratch must not reach the second's result. The cases cover split-KV partials (with the
-log-sum-exp), the key-norm table, and a launch that needs no scratch.
+log-sum-exp), the key-norm table (on causal grids that also deal their last programs at run time
+from the library's static ticket words, which allocate nothing either), and a launch that needs
+no scratch.
 """
 
 import math
