@@ -128,17 +128,49 @@ FA2_API int fa2_ablate_hbm_read(const void* src, int64_t bytes, uint32_t* out, i
 
 /*
  * fa2_ablate_tail_schedule - the dynamic tail fa2_attn_fwd gives a launch at the default
- * configuration (block_m 128, the default block_n, no split-KV): of its programs, the first
- * *static_blocks run in the static order and the last *tail_programs are dealt at run time to
- * *tail_workgroups workgroups (the spare ones find no program). All three are 0 when the launch
- * keeps the static order (non-causal, or fewer than two rounds of programs per XCD). Host-side
- * policy only, no GPU call. FA2_EINVAL for sizes
+ * configuration (block_m 128, the default block_n, no split-KV) on MI355X's topology (256 CUs,
+ * 8 XCDs): of its programs, the first *static_blocks run in the static order and the last
+ * *tail_programs are dealt at run time to *tail_workgroups workgroups (the spare ones find no
+ * program). All three are 0 when the launch keeps the static order (non-causal, or fewer than
+ * two rounds of programs per XCD). Host-side policy only, no GPU call. FA2_EINVAL for sizes
  * attention would reject (h_q % h_kv, head_dim, pack not 1 or the group).
  */
 FA2_API int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
                                      int32_t head_dim, int32_t causal, int32_t pack,
                                      int32_t* static_blocks, int32_t* tail_programs,
                                      int32_t* tail_workgroups);
+
+/* Words fa2_ablate_program_map writes to info. */
+#define FA2_ABLATE_MAP_INFO_WORDS 11
+
+/*
+ * fa2_ablate_program_map - which program every workgroup of a launch runs, computed on the CPU
+ * with the kernel's own code (program_of and the dynamic tail's ticket rules, which are
+ * __host__ __device__) on a device of `cus` CUs and `xcds` XCDs. The launch is fa2_attn_fwd's on
+ * contiguous tensors of these sizes (n_kv = n_q) at block_m rows and the default tile, without
+ * split-KV; static_order != 0 keeps the static order (FA2_ABLATE_STATIC_ORDER). The dynamic
+ * tail's workgroups take their tickets in a random order seeded by `seed`, with the kernel's
+ * wrapping increments emulated on the host.
+ *   programs  [grid][3] int32: (q tile, batch, first query head) of the program workgroup w runs,
+ *             or (-1, -1, -1) for a spare tail workgroup; program_words >= 3 x grid.
+ *   info      [FA2_ABLATE_MAP_INFO_WORDS]: grid (workgroups), static blocks, tail workgroups,
+ *             tail queues, private programs per queue, shared programs, unit chunk, log2 of
+ *             the XCDs the order uses, ticket words left nonzero after the launch (0: every word
+ *             wrapped back), q tiles per head group (n_tiles), head groups (batch x h_q / pack).
+ * No counterpart in the reference, and no GPU call: the CPU check that every program runs once.
+ */
+FA2_API int fa2_ablate_program_map(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                                   int32_t head_dim, int32_t causal, int32_t pack, int32_t block_m,
+                                   int32_t cus, int32_t xcds, int32_t static_order, uint32_t seed,
+                                   int32_t* programs, int64_t program_words, int32_t* info,
+                                   int32_t info_words);
+
+/*
+ * fa2_ablate_tail_launches - how many launches of this library (fa2_ablate_attn_fwd,
+ * fa2_ablate_timeline) ran with a dynamic tail so far in this process: a launch recorded under
+ * stream capture runs the static order and does not count. No counterpart in the reference.
+ */
+FA2_API long long fa2_ablate_tail_launches(void);
 
 /* Thread-local description of this library's last failure in this thread ("" if none). */
 FA2_API const char* fa2_ablate_last_error(void);

@@ -10,12 +10,16 @@
  * per call and keeps no per-call state. Launches are asynchronous on the given stream.
  *
  * Causal grids of at least two rounds of programs per XCD deal their last programs at run time
- * (a dynamic tail): their workgroups take tickets from a counter word in the library's own
- * device memory (a static array, loaded as zeros; no allocation), which every launch leaves at
- * zero again. There is one word per (device, stream), so calls on different streams and threads
- * may overlap freely. Launches recorded under stream capture, launches on the per-thread default
- * stream or on a stream of another device than the current one, and launches past 1024 streams
- * per device run the static order instead. Either way the output is the same, bit for bit.
+ * (a dynamic tail): their workgroups take tickets from counter words in the library's own device
+ * memory (a static array, loaded as zeros; no allocation), which every launch leaves at zero
+ * again. Each (device, stream) has its own set of words, so calls on different streams and
+ * threads may overlap freely; a launch that uses a set first makes its stream wait for an event
+ * the set's previous launch recorded, so a stream created with the handle of a destroyed one
+ * never meets the old stream's launches on the words. Launches recorded under stream capture,
+ * launches on the per-thread default stream or on a stream of another device than the current
+ * one, and launches past 256 streams per device run the static order instead. Either way the
+ * output is the same, bit for bit. The order of programs follows the device's CU and XCD counts,
+ * read once per device.
  *
  * Return convention: 0 on success, a negative FA2_E* code on a rejected argument or a
  * failed launch; fa2_last_error() then describes the failure (thread-local string).
@@ -122,9 +126,11 @@ FA2_API int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* o
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  *
  * The split-KV partials and, where it pays, the key-norm table live in a device array owned by
- * the library, FA2_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU until the
- * process ends. Its address is looked up on the first call on each device, which must be the
- * current device and the stream's. Every call on one GPU shares that array, so calls that
+ * the library, FA2_NOALLOC_SCRATCH_BYTES per GPU. The array sits in a device code object of its
+ * own, which the first fa2_attn_fwd_noalloc call on a GPU that needs scratch loads (measured on
+ * MI355X: 36 MiB less free device memory after that call, 4 MiB after the first other launch),
+ * and it stays until the process ends. Its address is looked up on that first call, which must
+ * run with the stream's device current. Every call on one GPU shares that array, so calls that
  * overlap on one GPU (two streams or two threads at once) race; serialise them. The caller still
  * passes q, k, v, out and lse.
  *

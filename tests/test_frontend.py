@@ -408,7 +408,8 @@ def test_measurement_library_exports_exactly_its_header():
     names = _exported(ABLATE_LIB)
     assert {n for n in names if n.startswith("fa2_")} == _c_names(ABLATE_HEADER) == {
         "fa2_ablate_attn_fwd", "fa2_ablate_timeline", "fa2_ablate_mfma_ceiling",
-        "fa2_ablate_hbm_read", "fa2_ablate_tail_schedule", "fa2_ablate_last_error"}
+        "fa2_ablate_hbm_read", "fa2_ablate_tail_schedule", "fa2_ablate_program_map",
+        "fa2_ablate_tail_launches", "fa2_ablate_last_error"}
     # the knockouts are compiled into it: kernel instances with the no_exp, no_softmax and
     # kv_l2 bits, and matmul_only (no_softmax | kv_l2); and the timeline instance (64)
     variants = {int(m.group(1)) for n in names for m in [re.search(r"ELb[01]ELi(\d+)EEEv", n)] if m}

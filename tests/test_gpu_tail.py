@@ -1,23 +1,29 @@
-"""The dynamic tail of causal grids (attn_fwd_host.hpp: tail_schedule, ticket_word).
+"""The dynamic tail of causal grids (attn_fwd_host.hpp: tail_schedule, acquire_tickets;
+attn_fwd_schedule.hpp: tail_pick).
 
 Where a causal grid has at least two rounds of programs per XCD, the last programs of every XCD's
 static order (program_of's XCD order, or its fallback order where the (batch, kv head) units do
-not split evenly over the 8 XCDs) are dealt at run time:
-each workgroup past the static part takes a ticket from a per-stream word with one atomic
-increment that wraps, so the word is zero again after every launch, and a few spare workgroups
-find no program and exit. Which workgroup runs a program changes from launch to launch; what the
-program computes does not. So:
+not split evenly over the 8 XCDs) are dealt at run time: each workgroup past the static part
+takes a ticket from its XCD's queue word (that XCD's own heavier tail programs) and, once its
+queue has none left for it, from the launch's shared word (the lightest tail programs, for
+whichever XCD asks). Every word is incremented a fixed number of times per launch and wraps, so it
+is zero again after every launch, and a few spare workgroups find no program and exit. Which
+workgroup runs a program changes from launch to launch; what the program computes does not. So:
 
 * the output equals the static order's (the measurement library's FA2_ABLATE_STATIC_ORDER) bit
   for bit, on shapes with and without GQA packing, ragged, at head_dim 64 and 128;
 * calls back to back, with tails of different sizes on one stream, keep that (every launch
-  leaves its word at zero for the next);
-* two streams running tails at the same time keep it (each stream has its own word);
+  leaves its words at zero for the next);
+* two streams running tails at the same time keep it (each stream has its own ticket set);
 * a launch recorded under stream capture keeps the static order (one graph can be instantiated
-  twice and run twice at once, which would share a word): its replays equal the eager calls,
-  which use the tail, bit for bit;
-* a stream destroyed and created again (the handle comes back; hipStreamDestroy waits for the
-  stream's queued work, so the old and new streams' launches never meet on the word) keeps it.
+  twice and run twice at once, which would share a set): the measurement library's count of tail
+  launches does not move while it is recorded, and its replays equal the eager calls, which use
+  the tail, bit for bit;
+* a stream destroyed with launches still queued and a new stream created at once (the handle can
+  come back while the old launches run): every ticket set's launch waits for the event its previous
+  launch recorded, so the old and new launches never share the words at once.
+
+The CPU tier (tests/test_schedule.py) checks the same ticket rules over thousands of shapes.
 """
 
 import pytest
@@ -122,16 +128,50 @@ def test_captured_launch_keeps_the_static_order_and_replays_exactly():
         q.copy_(nq), k.copy_(nk), v.copy_(nv)
         graph.replay()
         torch.cuda.synchronize()
-        want = attention(nq, nk, nv, causal=True)   # eager: the tail, on the stream's word
+        want = attention(nq, nk, nv, causal=True)   # eager: the tail, on the stream's words
+        torch.cuda.synchronize()
+        assert torch.equal(captured, want)
+
+
+def test_capture_records_the_static_order():
+    """The launch path's capture check, seen directly: the measurement library (the same host
+    code, compiled into it) counts the launches that took a ticket set. An eager launch counts;
+    one recorded under capture does not, and its replays equal the static order bit for bit."""
+    import ctypes
+
+    from ablation import ablate_lib, attention_ablate
+
+    lib = ablate_lib()
+    lib.fa2_ablate_tail_launches.restype = ctypes.c_longlong
+    lib.fa2_ablate_tail_launches.argtypes = []
+    q, k, v, _ = _inputs("gqa_d128", seed=4)
+    want = _static(q, k, v, False)
+    before = lib.fa2_ablate_tail_launches()
+    eager = attention_ablate(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert lib.fa2_ablate_tail_launches() == before + 1
+    assert torch.equal(eager, want)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            captured = attention_ablate(q, k, v, causal=True)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert lib.fa2_ablate_tail_launches() == before + 1   # recorded without a ticket set
+    for _ in range(2):
+        graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(captured, want)
 
 
 def test_a_new_stream_on_a_reused_handle_keeps_the_tail_exact():
-    """hipStreamDestroy frees the handle for the next stream created (the same address comes
-    back) once the stream's queued work has run; the new stream then starts from the word the old
-    one left at zero. Streams created and destroyed through the HIP runtime directly (torch pools
-    its own)."""
+    """A stream is destroyed with tail launches still queued on it (hipStreamDestroy need not
+    wait for them) and a new stream is created at once, which can get the same handle and so the
+    same ticket set; its launches wait for the event the old stream's last launch recorded, so
+    the two never use the set's words at once. Streams created and destroyed through the HIP
+    runtime directly (torch pools its own)."""
     import ctypes
     import math
 
@@ -140,18 +180,24 @@ def test_a_new_stream_on_a_reused_handle_keeps_the_tail_exact():
 
     hip = ctypes.CDLL("libamdhip64.so")
     hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
-    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
     hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipDeviceSynchronize.argtypes = []
     q, k, v, _ = _inputs("mha_ragged", seed=8)
     want = _static(q, k, v, False)
     torch.cuda.synchronize()
-    for _ in range(3):
+    outs, handles = [], []
+    for _ in range(4):
         h = ctypes.c_void_p()
         assert hip.hipStreamCreate(ctypes.byref(h)) == 0
-        out = torch.empty_like(q)
-        _lib.attn_fwd(q, k, v, out, True, 1, 128, 0, LOG2E / math.sqrt(q.shape[3]), h.value)
-        assert hip.hipStreamSynchronize(h) == 0
+        handles.append(h.value)
+        for _ in range(3):   # queued, not waited for, before the destroy
+            out = torch.empty_like(q)
+            _lib.attn_fwd(q, k, v, out, True, 1, 128, 0, LOG2E / math.sqrt(q.shape[3]), h.value)
+            outs.append(out)
         assert hip.hipStreamDestroy(h) == 0
+    assert hip.hipDeviceSynchronize() == 0
+    print(f"stream handles: {len(set(handles))} distinct of {len(handles)}", flush=True)
+    for out in outs:
         assert torch.equal(out, want)
 
 

@@ -4,8 +4,9 @@ a workspace of fa2_workspace_bytes_for(...) bytes. The checks use two calls in a
 library's shared scratch, the second with a smaller input, so the first call's leftovers in the
 scratch must not reach the second's result. The cases cover split-KV partials (with the
 log-sum-exp), the key-norm table (on causal grids that also deal their last programs at run time
-from the library's static ticket words, which allocate nothing either), and a launch that needs
-no scratch.
+from the library's static ticket words, which allocate nothing either), a launch that needs
+no scratch, and calls recorded under HIP graph capture (the callers the entry point is for) and
+replayed on new inputs.
 """
 
 import math
@@ -106,3 +107,45 @@ def test_noalloc_without_scratch_needs():
     torch.cuda.synchronize()
     assert torch.equal(out, attention(q, k, v, causal=True))
     _check_pair([(make_qkv(1, 8, 8, 1, 1024, 128, torch.bfloat16), False, 4, True)])
+
+
+@pytest.mark.parametrize("case", ["split_kv", "key_table"])
+def test_noalloc_under_graph_capture_replays_exactly(case):
+    """fa2_attn_fwd_noalloc recorded in a HIP graph (its device checks and the scratch lookup run
+    on the capturing stream; the graph keeps the scratch's address): every replay, on new inputs
+    copied into the captured tensors and with eager work and synchronisation in between, equals
+    fa2_attn_fwd_ex with a workspace, bit for bit. Split-KV (partials in the scratch, with the
+    log-sum-exp) and the key-norm table (C3's shape)."""
+    from fa2 import _lib
+
+    if case == "split_kv":
+        shape, causal, splits, want_lse = (8, 32, 8, 16, 4096, 128, torch.float16), False, 4, True
+    else:
+        shape, causal, splits, want_lse = (1, 32, 8, 8192, 8192, 128, torch.bfloat16), True, 1, False
+        assert _lib.workspace_bytes_for(1, 32, 8, 8192, 8192, 128, torch.bfloat16, True, 1) > 0
+    print(f"noalloc capture: {case} {shape}", flush=True)
+    q, k, v = make_qkv(*shape)
+    B, H_q, N_q, D = q.shape
+    out = torch.empty_like(q)
+    lse = torch.empty(B, H_q, N_q, dtype=torch.float32, device=q.device) if want_lse else None
+    _run_noalloc(q, k, v, causal, splits, want_lse)   # warm up: library load, scratch lookup
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            _lib.attn_fwd_noalloc(q, k, v, out, causal, 1, 128, 0, _scale(D), lse, splits,
+                                  stream.cuda_stream)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for seed in (1, 2, 3):
+        nq, nk, nv = make_qkv(*shape, seed=seed)
+        q.copy_(nq), k.copy_(nk), v.copy_(nv)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref_out, ref_lse, _ = _run_ex(nq, nk, nv, causal, splits, want_lse)   # eager, between
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out), seed
+        if want_lse:
+            assert torch.equal(lse, ref_lse), seed

@@ -1,6 +1,6 @@
 // attn_fwd_common.hpp - types and device helpers shared by the forward kernels:
 // the MFMA / conversion traits per element type, the LDS swizzle keys, lane-pair reductions,
-// the transposing LDS read, the HBM -> LDS buffer loads and the program renumbering.
+// the transposing LDS read and the HBM -> LDS buffer loads.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -210,82 +210,6 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// The workgroup -> (q tile, batch, first query head) decomposition. Workgroups are dealt to
-// the XCDs round-robin; block b runs on XCD b % 8.
-//   * When the (batch, kv head) units split evenly over the XCDs, each XCD owns a fixed set of
-//     whole units, so its L2 holds the K/V of the heads it works on (C3: HBM reads fell from
-//     635 to 139 MiB per launch). Causal: inside an XCD the order is q tile outermost (heaviest
-//     tile first) across all of its units, then unit, then the query-head groups sharing a KV
-//     head. Unit after unit instead started the last unit's heaviest tiles late and left the
-//     XCD's slots 22% idle on C2 (8 units per XCD): the q-tile-major order runs C2 12% faster,
-//     although its L2 now misses more (reads past L2 192 -> ~680 MiB per launch, ~2.6 TB/s).
-//     Non-causal programs all do the same work, so there the order is unit after unit: the
-//     programs in flight on an XCD then share one unit's K/V in its L2 (C4: four units per XCD
-//     read K/V 8.3x over in q-tile-major order).
-//   * Otherwise a fixed unit set per XCD would hand one XCD more of the heavy causal tiles than
-//     another (C5, 12 units over 8 XCDs: 15% more work on XCD 0). Then the order is q tile
-//     outermost over all units, heaviest first, and the round-robin dealing balances the XCDs.
-//     On causal grids of at most three programs per CU the first round decides the span, and
-//     heaviest-first hands each CU two of the heaviest programs. There the second program of
-//     every CU (blocks kCus .. 2 kCus - 1) is taken in reverse, so the heaviest programs share
-//     their CU with the lightest of the first round: +2.6% on C5 (672 programs), +6% on its
-//     head_dim-64 twin, +3.6% at 384 programs; from 896 programs on it no longer pays (+0.7%,
-//     -1.1% at 1344). Every program is computed alone, so the order never changes a result.
-struct Program {
-  int tile, b, hq0, hkv;
-};
-
-template <bool CAUSAL>
-__device__ __forceinline__ Program program_of(const Params& p, int block) {
-  const int progs_per_kv = p.group / p.pack;  // programs sharing one KV head per q tile
-  const int h_kv = p.h_q / p.group;
-  const int units = p.n_bh / progs_per_kv;    // batch * h_kv
-  int kv_index, t, h_in;
-  if (units % kXcds == 0) {
-    const int xcd = block % kXcds, slot = block / kXcds;
-    const int upx = units / kXcds;             // units per XCD
-    if (CAUSAL) {
-      // the XCD's units are taken unit_chunk at a time (the host's choice, a divisor of upx),
-      // q-tile-major inside each chunk: heavy tiles first, and the programs in flight read the
-      // K/V of a few units instead of all of the XCD's
-      const int cu = (p.unit_chunk > 0 && upx % p.unit_chunk == 0) ? p.unit_chunk : upx;
-      const int per_chunk = cu * progs_per_kv * p.n_tiles;  // programs of one chunk
-      const int ch = slot / per_chunk;
-      const int rs = slot - ch * per_chunk;
-      const int per_t = cu * progs_per_kv;     // programs per q tile of one chunk
-      t = rs / per_t;
-      const int r = rs - t * per_t;
-      kv_index = xcd * upx + ch * cu + r / progs_per_kv; // b * h_kv + hkv
-      h_in = r % progs_per_kv;
-    } else {
-      // every program has the same work: unit after unit, so that the XCD's programs in flight
-      // stream one unit's K/V through its L2 instead of several units' at once
-      const int per_u = p.n_tiles * progs_per_kv;  // programs of one unit
-      const int u = slot / per_u;
-      const int r = slot - u * per_u;
-      t = r / progs_per_kv;
-      h_in = r - t * progs_per_kv;
-      kv_index = xcd * upx + u;
-    }
-  } else {
-    const int grid = p.n_tiles * p.n_bh;
-    if (CAUSAL && grid <= 3 * kCus && block >= kCus) {
-      const int end = min(grid, 2 * kCus);
-      if (block < end) block = kCus + (end - 1 - block);
-    }
-    t = block / p.n_bh;
-    const int r = block - t * p.n_bh;
-    kv_index = r / progs_per_kv;
-    h_in = r - kv_index * progs_per_kv;
-  }
-  Program pr;
-  pr.tile = CAUSAL ? p.n_tiles - 1 - t : t;
-  pr.b = kv_index / h_kv;
-  pr.hkv = kv_index - pr.b * h_kv;
-  pr.hq0 = pr.hkv * p.group + h_in * p.pack;
-  return pr;
 }
 
 }  // namespace fa2

@@ -41,8 +41,18 @@
 #pragma once
 
 #include "attn_fwd_common.hpp"
+#include "attn_fwd_schedule.hpp"
 
 namespace fa2 {
+
+// The dynamic tail's program of tail workgroup `block` (tail_pick), with agent-scope atomic
+// increments of the launch's ticket words. Returns the block whose program to run, or -1.
+__device__ __forceinline__ int take_tail_program(const Params& p, int block) {
+  return tail_pick(p, block, [&](int word, uint32_t limit) {
+    return __builtin_amdgcn_atomic_inc32(p.tickets + word * kTicketStride, limit,
+                                         __ATOMIC_RELAXED, "agent");
+  });
+}
 
 // ---------------------------------------------------------------------------------
 // the kernel
@@ -94,17 +104,15 @@ void attn_fwd_kernel(const Params p) {
   // split-KV: consecutive workgroups are the splits of one program
   const int split = p.splits > 1 ? (int)blockIdx.x % p.splits : 0;
   int block = p.splits > 1 ? (int)blockIdx.x / p.splits : (int)blockIdx.x;
-  // dynamic tail: the workgroup's program is the next ticket, taken by one lane and passed to
-  // the others through LDS; tickets past the tail's programs have nothing to run
+  // dynamic tail: one lane takes the workgroup's tickets (its XCD's queue first, then the shared
+  // pool) and passes the program it won to the others through LDS; -1: nothing left to run
   if (block >= p.static_blocks) {
-    __shared__ int ticket;
-    if (tid == 0)
-      ticket = (int)__builtin_amdgcn_atomic_inc32(p.tickets, (uint32_t)(p.tail_wgs - 1),
-                                                  __ATOMIC_RELAXED, "agent");
+    __shared__ int picked;
+    if (tid == 0) picked = take_tail_program(p, block);
     __syncthreads();
-    const int t = __builtin_amdgcn_readfirstlane(ticket);
-    if (t >= p.tail_programs) return;
-    block = p.static_blocks + t;
+    const int b = __builtin_amdgcn_readfirstlane(picked);
+    if (b < 0) return;
+    block = b;
   }
   const Program pr = program_of<CAUSAL>(p, block);
 

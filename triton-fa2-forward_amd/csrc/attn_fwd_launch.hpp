@@ -29,6 +29,12 @@ int launch_combine(int dtype, int head_dim, const CombineParams& c, hipStream_t 
 int launch_key_norm(int dtype, int head_dim, const KeyNormParams& k, unsigned grid,
                     hipStream_t stream);
 
+// Devices the no-allocation scratch table covers (fa2_scratch.hip).
+constexpr int kScratchDevices = 64;
+// The device address of fa2_attn_fwd_noalloc's scratch array on device `dev`, which must be the
+// current device: looked up once per device (hipGetSymbolAddress) and kept. Returns a hipError_t.
+hipError_t noalloc_scratch(int dev, void** out);
+
 #define FA2_DECLARE_LAUNCH(DT, D)                                                          \
   extern template int launch_attn_fwd<DT, D>(const Params&, int, int, bool, unsigned, \
                                              hipStream_t);

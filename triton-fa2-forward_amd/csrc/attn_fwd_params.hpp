@@ -5,11 +5,17 @@
 
 namespace fa2 {
 
-// Number of XCDs (each with its own L2) that the hardware deals workgroups to round-robin.
+// The topology the program order is tuned on (MI355X): 8 XCDs, each with its own L2, that the
+// hardware deals workgroups to round-robin (block b runs on XCD b % 8), and 256 CUs. With two
+// workgroups per CU, the dispatcher's first round places block b and block b + 256 on the same
+// CU (measured with the hardware CU id). The host reads the real counts from the device and
+// passes them in Params (xcd_shift, cus); other counts get the same order rules with their own
+// numbers (attn_fwd_schedule.hpp).
 constexpr int kXcds = 8;
-// Compute units (8 XCDs x 32). With two workgroups per CU, the dispatcher's first round places
-// block b and block b + kCus on the same CU (measured with the hardware CU id).
 constexpr int kCus = 256;
+// Largest XCD count the XCD-aware order and the per-XCD tail queues serve; a device that reports
+// more, or a count that is not a power of two, is ordered as one XCD.
+constexpr int kMaxXcds = 16;
 
 // Keys per entry of the key-norm table (attn_key_norm.hip): one workgroup of the key-norm pass
 // each (C3: 1024 workgroups), and at most three entries per 128-row causal program's own rows.
@@ -35,15 +41,27 @@ struct Params {
   // Causal grids whose (batch, kv head) units split evenly over the XCDs: each XCD runs its
   // units unit_chunk at a time (a divisor of its unit count), q-tile-major inside a chunk.
   int32_t unit_chunk;
-  // Dynamic tail (causal grids; the host's tail_schedule): the workgroups from static_blocks on
-  // each take one ticket from *tickets with an agent-scope atomic increment that wraps at
-  // tail_wgs - 1, so that the word is zero again once the launch has run. Ticket t below
-  // tail_programs runs program static_blocks + t of the static order; the others exit at once.
+  // Topology of the device the launch runs on: log2 of its XCD count (a power of two, at most
+  // kMaxXcds) and its CU count. They drive program_of's order only, never a result.
+  int32_t xcd_shift;
+  int32_t cus;
+  // Dynamic tail (causal grids; the host's tail_schedule, attn_fwd_schedule.hpp): the workgroups
+  // from static_blocks on are dealt the last programs of the static order at run time through the
+  // ticket words at *tickets. Tail workgroup w belongs to queue w % tail_queues (its XCD: block b
+  // runs on XCD b % 8). It first takes a ticket from its queue's word; ticket t below
+  // tail_private runs its XCD's program static_blocks + t * tail_queues + queue (locality: that
+  // XCD's L2 holds the unit's K/V). Otherwise it takes a ticket u from the shared word; u below
+  // tail_shared runs program static_blocks + tail_queues * tail_private + u, whichever XCD asks
+  // (balance: a fast XCD takes more of them); the rest exit at once. Every word is incremented
+  // by a fixed number of workgroups per launch (tail_wgs / tail_queues for a queue, the rest for
+  // the shared word) and wraps there, so it is zero again when the launch ends.
   // No tail: static_blocks = INT32_MAX (read beside the grid fields, so that the check costs the
   // prologue no load of its own) and workgroup b runs program b.
   int32_t static_blocks;
   int32_t tail_wgs;
-  int32_t tail_programs;
+  int32_t tail_queues;
+  int32_t tail_private;  // programs per queue
+  int32_t tail_shared;   // programs in the shared pool
   float qk_scale;   // sm_scale * log2(e)
   // Optional outputs beyond the reference's:
   float* lse;        // [B, H_q, N_q] natural-log log-sum-exp of the scaled scores, or null;
@@ -64,12 +82,19 @@ struct Params {
   // more than kBoundTau (Cauchy-Schwarz) and then skips the per-tile row max.
   const float* key_norm2;  // [B * H_kv][key_chunks]
   int32_t key_chunks;      // ceil(n_kv / kKeyChunk)
-  uint32_t* tickets;  // the tail's ticket word (read only past static_blocks)
+  // The tail's ticket words (read only past static_blocks): the shared word at tickets[0], queue
+  // x's at tickets[(1 + x) * kTicketStride].
+  uint32_t* tickets;
   // Measurement library only (the timeline variant): kTimelineWords uint64 per program,
   // indexed by the program's place in the static order. Null, and never read, in the product's
   // instances.
   uint64_t* timeline;
 };
+
+// uint32 words between two ticket words of a launch: each on its own 64-byte line.
+constexpr int kTicketStride = 16;
+// Ticket words per launch: the shared word and one per XCD queue.
+constexpr int kTicketWordsPerSet = 1 + kMaxXcds;
 
 // Words per workgroup of the timeline variant: entry, prologue done (first barrier), tile loop
 // done, stores done (s_memrealtime, 100 MHz), the workgroup's K/V tile count, and its hardware

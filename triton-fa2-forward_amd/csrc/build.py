@@ -124,11 +124,13 @@ def build(jobs=8, verbose=False):
                        "-o", os.path.join(OBJ_DIR, name + ".o")])
     api = [cc, *common_flags(), "-c", os.path.join(CSRC, "fa2_fwd.hip"),
            "-o", os.path.join(OBJ_DIR, "fa2_fwd.o")]
+    scratch = [cc, *common_flags(), "-c", os.path.join(CSRC, "fa2_scratch.hip"),
+               "-o", os.path.join(OBJ_DIR, "fa2_scratch.o")]
     ablate_api = [cc, *common_flags(), "-c", os.path.join(CSRC, "fa2_ablate.hip"),
                   "-o", os.path.join(OBJ_DIR, "fa2_ablate.o")]
     ceiling = [cc, *common_flags(), "-c", os.path.join(CSRC, "mfma_ceiling.hip"),
                "-o", os.path.join(OBJ_DIR, "mfma_ceiling.o")]
-    everything = units + shared + [api] + ablate_units + [ablate_api, ceiling]
+    everything = units + shared + [api, scratch] + ablate_units + [ablate_api, ceiling]
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         errs = list(ex.map(lambda cmd: _run(cmd, verbose), everything))
 
@@ -146,7 +148,7 @@ def build(jobs=8, verbose=False):
         os.replace(path + ".tmp", path)
 
     shared_objs = [u[-1] for u in shared]
-    link([u[-1] for u in units] + shared_objs + [api[-1]], LIB_PATH)
+    link([u[-1] for u in units] + shared_objs + [api[-1], scratch[-1]], LIB_PATH)
     link([u[-1] for u in ablate_units] + shared_objs + [ablate_api[-1], ceiling[-1]],
          ABLATE_LIB_PATH)
     build_capi_check(verbose)

@@ -3,8 +3,11 @@
 // the product (attn_fwd_host.hpp, compiled into this library separately).
 #include <hip/hip_runtime.h>
 
+#include <vector>
+
 #include "attn_fwd_ablate.hpp"
 #include "attn_fwd_host.hpp"
+#include "attn_fwd_schedule.hpp"
 #include "fa2_ablate.h"
 
 namespace {
@@ -23,6 +26,24 @@ int launch_ablate(int dtype, int di, const Params& p, int waves, int block_n, bo
     case 6: return fa2::launch_attn_fwd_ablate<1, 64>(p, variant, causal, grid, s);
     default: return fa2::launch_attn_fwd_ablate<1, 128>(p, variant, causal, grid, s);
   }
+}
+
+// The plan of a launch of contiguous [B, H, N, D] tensors at block_m rows and the default
+// tile, without a workspace (no split-KV, no key-norm table), on `topo`. No device call.
+int plan_default(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t head_dim,
+                 int32_t causal, int32_t pack, int32_t block_m, const Topology& topo,
+                 bool static_order, LaunchPlan* pl) {
+  if (batch < 1 || h_q < 1 || h_kv < 1 || n_q < 1 || h_q % h_kv)
+    return fail(FA2_EINVAL, "bad sizes: batch=%d h_q=%d h_kv=%d n_q=%d", batch, h_q, h_kv, n_q);
+  const int64_t d = head_dim;
+  const int64_t sq[4] = {(int64_t)h_q * n_q * d, (int64_t)n_q * d, d, 1};
+  const int64_t sk[4] = {(int64_t)h_kv * n_q * d, (int64_t)n_q * d, d, 1};
+  // stand-in device addresses: the plan checks their alignment and never dereferences them
+  void* const fake = reinterpret_cast<void*>(uintptr_t(1) << 20);
+  const LaunchArgs a{fake, fake, fake, fake, sq, sk, sk, sq, batch, h_q, h_kv, n_q, n_q,
+                     head_dim, FA2_DTYPE_BF16, causal, pack, block_m, 0, 1.0f, nullptr, 1,
+                     nullptr, 0, 0, nullptr, 0, static_order};
+  return plan_launch(a, topo, pl);
 }
 
 }  // namespace
@@ -46,9 +67,10 @@ int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
     return fail(FA2_EINVAL, "variant 0x%x is not one of the built timing variants",
                 (unsigned)variant);
   }
-  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
-                       n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
-                       nullptr, 0, variant, launch_ablate, stream, nullptr, 0, static_order);
+  const LaunchArgs a{q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                     n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
+                     nullptr, 0, variant, nullptr, 0, static_order};
+  return attn_fwd_impl(a, launch_ablate, stream);
 }
 
 int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
@@ -61,10 +83,10 @@ int fa2_ablate_timeline(const void* q, const void* k, const void* v, void* out,
   if (!records) return fail(FA2_EINVAL, "null timeline buffer");
   if (reinterpret_cast<uintptr_t>(records) & 7u)
     return fail(FA2_EALIGN, "the timeline buffer must be 8-byte aligned");
-  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
-                       n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
-                       nullptr, 0, fa2::kVariantTimeline, launch_ablate, stream, records,
-                       record_words);
+  const LaunchArgs a{q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                     n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
+                     nullptr, 0, fa2::kVariantTimeline, records, record_words, false};
+  return attn_fwd_impl(a, launch_ablate, stream);
 }
 
 int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
@@ -74,27 +96,75 @@ int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n
   g_err[0] = '\0';
   if (!static_blocks || !tail_programs || !tail_workgroups) return fail(FA2_EINVAL, "null output");
   *static_blocks = *tail_programs = *tail_workgroups = 0;
-  if (batch < 1 || h_q < 1 || h_kv < 1 || n_q < 1 || h_q % h_kv)
-    return fail(FA2_EINVAL, "bad sizes: batch=%d h_q=%d h_kv=%d n_q=%d", batch, h_q, h_kv, n_q);
-  if (dim_index(head_dim) < 0)
-    return fail(FA2_EINVAL, "head_dim must be a power of two in [16, 128], got %d", head_dim);
-  const int group = h_q / h_kv;
-  if (pack != 1 && pack != group)
-    return fail(FA2_EINVAL, "pack must be 1 or the GQA group %d, got %d", group, pack);
-  if (128 % pack)
-    return fail(FA2_EINVAL, "pack_gqa needs BLOCK_M (128) to be a multiple of the group (%d)", pack);
-  // attn_fwd_impl's grid at block_m 128 (4 waves) and the default K/V tile
-  const int64_t n_tiles = ((int64_t)n_q * pack + 127) / 128;
-  const int64_t n_bh = (int64_t)batch * (h_q / pack);
-  const int64_t units = n_bh / (group / pack);
-  const TailSchedule ts =
-      tail_schedule(causal != 0, 1, 4, units, group / pack, n_tiles,
-                    unit_chunk(units, n_q, head_dim), head_dim, tile_n(0, head_dim));
-  *static_blocks = ts.static_blocks;
-  *tail_programs = ts.tail_programs;
-  *tail_workgroups = ts.tail_wgs;
+  LaunchPlan pl;
+  const int rc = plan_default(batch, h_q, h_kv, n_q, head_dim, causal, pack, 128, Topology{}, false,
+                              &pl);
+  if (rc != FA2_OK) return rc;
+  *static_blocks = pl.tail.static_blocks;
+  *tail_programs = pl.tail.programs();
+  *tail_workgroups = pl.tail.tail_wgs;
   return 0;
 }
+
+int fa2_ablate_program_map(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
+                           int32_t head_dim, int32_t causal, int32_t pack, int32_t block_m,
+                           int32_t cus, int32_t xcds, int32_t static_order, uint32_t seed,
+                           int32_t* programs, int64_t program_words, int32_t* info,
+                           int32_t info_words) {
+  g_err[0] = '\0';
+  if (!programs || !info || info_words < FA2_ABLATE_MAP_INFO_WORDS)
+    return fail(FA2_EINVAL, "null output or info shorter than %d words", FA2_ABLATE_MAP_INFO_WORDS);
+  if (cus < 1 || xcds < 1) return fail(FA2_EINVAL, "cus and xcds must be positive");
+  LaunchPlan pl;
+  const int rc = plan_default(batch, h_q, h_kv, n_q, head_dim, causal, pack, block_m,
+                              make_topology(cus, xcds), static_order != 0, &pl);
+  if (rc != FA2_OK) return rc;
+  const int64_t grid = pl.empty ? 0 : pl.grid;
+  if (program_words < 3 * grid)
+    return fail(FA2_EINVAL, "the map needs %lld words for %lld workgroups, got %lld",
+                (long long)(3 * grid), (long long)grid, (long long)program_words);
+  Params& p = pl.p;
+  if (pl.tail.tail_wgs > 0) apply_tail(pl, nullptr);
+  // the kernel's program choice, workgroup by workgroup: the static order, then the tail's
+  // tickets in a seeded random order of its workgroups (any order is one the hardware may take)
+  uint32_t words[fa2::kTicketWordsPerSet] = {};
+  auto inc = [&](int word, uint32_t limit) {
+    const uint32_t old = words[word];
+    words[word] = old >= limit ? 0u : old + 1u;
+    return old;
+  };
+  const int64_t first_tail = pl.tail.tail_wgs > 0 ? p.static_blocks : grid;
+  std::vector<int32_t> order;
+  for (int64_t w = first_tail; w < grid; ++w) order.push_back((int32_t)w);
+  uint64_t st = 0x9e3779b97f4a7c15ull ^ seed;
+  for (size_t i = order.size(); i > 1; --i) {  // Fisher-Yates with a 64-bit LCG
+    st = st * 6364136223846793005ull + 1442695040888963407ull;
+    std::swap(order[i - 1], order[(size_t)((st >> 33) % i)]);
+  }
+  auto put = [&](int64_t w, int block) {
+    int32_t* o = programs + 3 * w;
+    if (block < 0) {
+      o[0] = o[1] = o[2] = -1;
+      return;
+    }
+    const fa2::Program pr = causal ? fa2::program_of<true>(p, block) : fa2::program_of<false>(p, block);
+    o[0] = pr.tile;
+    o[1] = pr.b;
+    o[2] = pr.hq0;
+  };
+  for (int64_t w = 0; w < first_tail; ++w) put(w, (int)w);
+  for (int32_t w : order) put(w, fa2::tail_pick(p, w, inc));
+  int nonzero = 0;
+  for (uint32_t x : words) nonzero += x != 0;
+  const int32_t vals[FA2_ABLATE_MAP_INFO_WORDS] = {
+      (int32_t)grid, pl.tail.tail_wgs > 0 ? pl.tail.static_blocks : (int32_t)grid,
+      pl.tail.tail_wgs, pl.tail.queues, pl.tail.private_per_queue, pl.tail.shared,
+      p.unit_chunk, p.xcd_shift, nonzero, p.n_tiles, p.n_bh};
+  for (int i = 0; i < FA2_ABLATE_MAP_INFO_WORDS; ++i) info[i] = vals[i];
+  return 0;
+}
+
+long long fa2_ablate_tail_launches(void) { return g_tail_launches.load(); }
 
 int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, float* out,
                             int64_t out_words, void* stream) {

@@ -7,9 +7,6 @@
 // launch it out of bounds.
 #include <hip/hip_runtime.h>
 
-#include <atomic>
-#include <mutex>
-
 #include "attn_fwd_host.hpp"
 
 namespace {
@@ -120,62 +117,17 @@ int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* out,
                     int32_t head_dim, int32_t dtype, int32_t causal, int32_t pack,
                     int32_t block_m, int32_t block_n, float qk_scale, float* lse,
                     int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream) {
-  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
-                       n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale, lse,
-                       num_splits, workspace, workspace_bytes, 0, launch, stream);
+  const LaunchArgs a{q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                     n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale, lse,
+                     num_splits, workspace, workspace_bytes, 0, nullptr, 0, false};
+  return attn_fwd_impl(a, launch, stream);
 }
 
 }  // extern "C"
 
-// ---- the no-allocation entry point: its workspace is this library's own device memory.
-// One copy per GPU, alive until the process ends; every call on a GPU shares it, so calls that
-// overlap on one GPU (two streams, two threads) race. Nothing in it needs clearing between
-// calls: the split-KV partials and the key-norm table are written in full before they are read.
-static __device__ __align__(256) unsigned char scratch[FA2_NOALLOC_SCRATCH_BYTES];
-
-namespace {
-
-constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
-
-// Device address of `scratch` on the GPU that `stream` runs on, which must be the current one.
-// Looked up once per device (hipGetSymbolAddress with that device current) and kept: the array's
-// host-side name is only a stand-in and must never reach a kernel.
-int scratch_on_stream_device(void* stream, void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(FA2_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
-  if (stream) {
-    hipDevice_t sdev = -1;
-    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
-    if (e != hipSuccess)
-      return fail(FA2_ELAUNCH, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
-    if (sdev != dev)
-      return fail(FA2_EINVAL,
-                  "the stream runs on device %d but device %d is current; make it current", sdev,
-                  dev);
-  }
-  if (dev < 0 || dev >= kMaxScratchDevices)
-    return fail(FA2_EINVAL, "device %d is past the %d devices the scratch table covers", dev,
-                kMaxScratchDevices);
-  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
-  if (!p) {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
-    if (!p) {
-      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-      if (e != hipSuccess || !p)
-        return fail(FA2_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
-                    hipGetErrorString(e));
-      g_scratch_ptr[dev].store(p, std::memory_order_release);
-    }
-  }
-  *out = p;
-  return FA2_OK;
-}
-
-}  // namespace
+// ---- the no-allocation entry point. Its workspace is the library's own device array, defined in
+// fa2_scratch.hip: a translation unit of its own, so that its 32 MiB belong to a code object that
+// only this entry point's address lookup loads.
 
 extern "C" {
 
@@ -200,12 +152,31 @@ int fa2_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
   if (use > (size_t)FA2_NOALLOC_SCRATCH_BYTES) use = need;
   void* ws = nullptr;
   if (use > 0) {
-    const int rc = scratch_on_stream_device(stream, &ws);
-    if (rc != FA2_OK) return rc;
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(FA2_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (stream) {
+      hipDevice_t sdev = -1;
+      e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+      if (e != hipSuccess)
+        return fail(FA2_ELAUNCH, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+      if (sdev != dev)
+        return fail(FA2_EINVAL,
+                    "the stream runs on device %d but device %d is current; make it current",
+                    sdev, dev);
+    }
+    if (dev < 0 || dev >= fa2::kScratchDevices)
+      return fail(FA2_EINVAL, "device %d is past the %d devices the scratch table covers", dev,
+                  fa2::kScratchDevices);
+    e = fa2::noalloc_scratch(dev, &ws);
+    if (e != hipSuccess || !ws)
+      return fail(FA2_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
   }
-  return attn_fwd_impl(q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
-                       n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale, lse,
-                       num_splits, ws, use, 0, launch, stream);
+  const LaunchArgs a{q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
+                     n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale, lse,
+                     num_splits, ws, use, 0, nullptr, 0, false};
+  return attn_fwd_impl(a, launch, stream);
 }
 
 }  // extern "C"
