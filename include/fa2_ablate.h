@@ -33,6 +33,10 @@ extern "C" {
 #define FA2_ABLATE_NO_SOFTMAX 16       /* no mask, max, exp, sum or rescale: O = (Q K^T) V (:7)  */
 #define FA2_ABLATE_KV_L2 32            /* every K/V tile load reads the first tile again, so it
                                           hits L2 instead of HBM (:8-9)                          */
+/* Not in the reference: K/V tiles from the third on are not loaded (every tile's products read
+ * whichever of the first two tiles its LDS buffer holds; output wrong on purpose): what the
+ * HBM/L2 -> LDS staging of K/V costs beyond the first tiles. */
+#define FA2_ABLATE_NO_KV_STAGING 256
 /* Not a kernel switch and not in the reference: the launch keeps the static order of programs
  * (workgroup b runs program b) where fa2_attn_fwd deals a causal grid's last programs at run
  * time (its dynamic tail). Combines with any variant; the output is the same bit for bit. */
@@ -51,6 +55,7 @@ extern "C" {
  *              FA2_ABLATE_NO_SOFTMAX                      no_softmax
  *              FA2_ABLATE_KV_L2                           kv_l2
  *              FA2_ABLATE_NO_SOFTMAX | FA2_ABLATE_KV_L2   matmul_only
+ *              FA2_ABLATE_NO_KV_STAGING                   no_kv_staging (not in the reference)
  *            each optionally with FA2_ABLATE_STATIC_ORDER;
  *            other bit sets are rejected (FA2_EINVAL).
  * The other arguments are fa2_attn_fwd's (include/fa2_fwd.h), with the same checks. Runs at the
@@ -148,9 +153,12 @@ FA2_API int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, i
  * with the kernel's own code (program_of and the dynamic tail's ticket rules, which are
  * __host__ __device__) on a device of `cus` CUs and `xcds` XCDs. The launch is fa2_attn_fwd's on
  * contiguous tensors of these sizes (n_kv = n_q) at block_m rows and the default tile, without
- * split-KV; static_order != 0 keeps the static order (FA2_ABLATE_STATIC_ORDER). The dynamic
- * tail's workgroups take their tickets in a random order seeded by `seed`, with the kernel's
- * wrapping increments emulated on the host.
+ * split-KV; static_order != 0 keeps the static order (FA2_ABLATE_STATIC_ORDER).
+ * tail_private_pct is the share of each XCD's tail programs its own queue holds: -1 for the
+ * library's (what fa2_attn_fwd launches), or 0..100 to plan another build's policy (the
+ * FA2_TAIL_PRIVATE_PCT a variant build is compiled with). The dynamic tail's workgroups take
+ * their tickets in a random order seeded by `seed`, with the kernel's wrapping increments
+ * emulated on the host.
  *   programs  [grid][3] int32: (q tile, batch, first query head) of the program workgroup w runs,
  *             or (-1, -1, -1) for a spare tail workgroup; program_words >= 3 x grid.
  *   info      [FA2_ABLATE_MAP_INFO_WORDS]: grid (workgroups), static blocks, tail workgroups,
@@ -161,9 +169,9 @@ FA2_API int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, i
  */
 FA2_API int fa2_ablate_program_map(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
                                    int32_t head_dim, int32_t causal, int32_t pack, int32_t block_m,
-                                   int32_t cus, int32_t xcds, int32_t static_order, uint32_t seed,
-                                   int32_t* programs, int64_t program_words, int32_t* info,
-                                   int32_t info_words);
+                                   int32_t cus, int32_t xcds, int32_t static_order,
+                                   int32_t tail_private_pct, uint32_t seed, int32_t* programs,
+                                   int64_t program_words, int32_t* info, int32_t info_words);
 
 /*
  * fa2_ablate_tail_launches - how many launches of this library (fa2_ablate_attn_fwd,

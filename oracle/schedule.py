@@ -28,7 +28,7 @@ import numpy as np
 
 KCUS, KXCDS, KMAX_XCDS = 256, 8, 16
 CHUNK_KV_BYTES = 8 << 20
-TAIL_PRIVATE_PCT = 50
+TAIL_PRIVATE_PCT = 0   # the shipped policy; builds can differ (FA2_TAIL_PRIVATE_PCT)
 
 
 def make_topology(cus, xcds):

@@ -7,7 +7,7 @@ reference tests its knockout copy (tests/test_ablation.py:16-48):
 * mask_every_tile only adds work: still bit for bit;
 * scale_first, and both switches together (the reference's "before_fixes"), still compute
   attention: the 2x-SDPA rule against the fp64 oracle;
-* the work-skipping knockouts (no_exp, no_softmax, kv_l2, matmul_only) change the output
+* the work-skipping knockouts (no_exp, no_softmax, kv_l2, matmul_only, no_kv_staging) change the output
   (tests/test_ablation.py:28-34), on both of the kernel's tile loops (software-pipelined at
   head_dim 64, one tile at a time otherwise), causal or not.
 """
@@ -84,15 +84,16 @@ def test_scale_first_changes_only_rounding():
 
 
 @pytest.mark.parametrize("knobs", [{"no_exp": True}, {"no_softmax": True}, {"kv_l2": True},
-                                   {"no_softmax": True, "kv_l2": True}],
-                         ids=["no_exp", "no_softmax", "kv_l2", "matmul_only"])
+                                   {"no_softmax": True, "kv_l2": True}, {"no_kv_staging": True}],
+                         ids=["no_exp", "no_softmax", "kv_l2", "matmul_only", "no_kv_staging"])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype,D", [(torch.float16, 16), (torch.bfloat16, 32),
                                      (torch.float16, 64), (torch.bfloat16, 64),
                                      (torch.bfloat16, 128)])
 def test_knockouts_change_the_output(knobs, causal, dtype, D):
     """300 keys span three tiles at every head dim (128-key tiles at 16, 64-key tiles above), so
-    kv_l2's repeated first tile differs from the real ones."""
+    kv_l2's repeated first tile differs from the real ones, and no_kv_staging's third tile is a
+    stale copy of the first."""
     from fa2.kernel import attention
 
     q, k, v = make_qkv(BATCH, 4, 2, 300, 300, D, dtype)

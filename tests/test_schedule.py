@@ -42,18 +42,18 @@ def _map_fn():
     fn = ablate_lib().fa2_ablate_program_map
     i32 = ctypes.c_int32
     fn.restype = ctypes.c_int
-    fn.argtypes = [i32] * 11 + [ctypes.c_uint32, ctypes.POINTER(i32), ctypes.c_int64,
+    fn.argtypes = [i32] * 12 + [ctypes.c_uint32, ctypes.POINTER(i32), ctypes.c_int64,
                                 ctypes.POINTER(i32), i32]
     return fn
 
 
-def library_map(fn, shape, seed=0):
+def library_map(fn, shape, seed=0, private_pct=-1):
     B, hq, hkv, n, d, causal, pack, bm, cus, xcds, static = shape
     groups = B * (hq // pack) * ((n * pack + bm - 1) // bm)
     cap = 3 * (groups + groups // 10 + 64)
     out = np.full(cap, -7, dtype=np.int32)
     info = np.zeros(INFO_WORDS, dtype=np.int32)
-    rc = fn(B, hq, hkv, n, d, causal, pack, bm, cus, xcds, static, seed,
+    rc = fn(B, hq, hkv, n, d, causal, pack, bm, cus, xcds, static, private_pct, seed,
             out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), cap,
             info.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), INFO_WORDS)
     assert rc == 0, shape
@@ -93,10 +93,10 @@ def sweep_shapes(count=3000, seed=1):
     return shapes
 
 
-def restated(shape, plant=None):
+def restated(shape, plant=None, private_pct=sch.TAIL_PRIVATE_PCT):
     B, hq, hkv, n, d, causal, pack, bm, cus, xcds, static = shape
     plan, progs, tail_blocks = sch.launch_programs(B, hq, hkv, n, d, bool(causal), pack, bm, cus,
-                                                   xcds, plant=plant)
+                                                   xcds, private_pct=private_pct, plant=plant)
     if static:
         plan.update(static_blocks=0, tail_wgs=0, queues=1, private=0, shared=0)
         tail_blocks = tail_blocks[:0]
@@ -109,13 +109,17 @@ def shapes():
 
 
 @needs_ablate
-def test_library_map_runs_every_program_once_and_equals_the_restatement(shapes):
+@pytest.mark.parametrize("private_pct", [-1, 50, 100])
+def test_library_map_runs_every_program_once_and_equals_the_restatement(shapes, private_pct):
+    """-1: the shipped policy (one shared pool); 50 and 100: per-XCD queues as variant builds
+    plan them (FA2_TAIL_PRIVATE_PCT), the kernel's queue rules included."""
     fn = _map_fn()
+    pct = sch.TAIL_PRIVATE_PCT if private_pct < 0 else private_pct
     tails = fallback_tails = queued = 0
     for i, shape in enumerate(shapes):
         B, hq, hkv, n, d, causal, pack, bm, cus, xcds, static = shape
-        got, info = library_map(fn, shape, seed=i)
-        plan, progs, tail_blocks = restated(shape)
+        got, info = library_map(fn, shape, seed=i, private_pct=private_pct)
+        plan, progs, tail_blocks = restated(shape, private_pct=pct)
         # the plan: grid decomposition, unit chunk, topology and tail policy
         for key in ("n_tiles", "n_bh", "unit_chunk", "xcd_shift", "tail_wgs", "queues", "private",
                     "shared"):
@@ -146,18 +150,21 @@ def test_library_map_runs_every_program_once_and_equals_the_restatement(shapes):
             run = got
         errs = sch.coverage_errors(run, B, hq, pack, plan["n_tiles"])
         assert errs == [], (shape, errs)
-    # the sweep reached both kinds of tail (per-XCD queues and the fallback's shared pool)
-    assert tails > 200 and queued > 50 and fallback_tails > 50, (tails, queued, fallback_tails)
+    # the sweep reached tails of every kind (per-XCD queues where the policy has them, and the
+    # shared pool alone)
+    assert tails > 200 and fallback_tails > 50, (tails, fallback_tails)
+    assert (queued > 50) == (pct > 0), (queued, pct)
 
 
 @pytest.mark.parametrize("plant", ["chunk", "reverse", "tail"])
 def test_planted_mistakes_fail_the_coverage_check(shapes, plant):
     """The exactly-once check must see an off-by-one in the unit chunk, the reversed second round
-    or the tail's private blocks: each planted in the restatement fails on the sweep."""
+    or the tail's private blocks (per-XCD queues, as a 50% build plans them): each planted in
+    the restatement fails on the sweep."""
     failed = 0
     for shape in shapes:
         B, hq, hkv, n, d, causal, pack, bm, cus, xcds, static = shape
-        plan, progs, tail_blocks = restated(shape, plant=plant)
+        plan, progs, tail_blocks = restated(shape, plant=plant, private_pct=50)
         if plan["tail_wgs"]:
             run = np.concatenate([progs[:plan["static_blocks"]], progs[tail_blocks]])
         else:
@@ -184,7 +191,11 @@ def test_topology_rules():
                                (228, 6): 0, (256, 32): 0, (100, 8): 0, (256, 16): 4}.items():
         _, info = library_map(fn, (1, 32, 8, 1024, 128, 1, 1, 128, cus, xcds, 0))
         assert info["xcd_shift"] == shift == sch.make_topology(cus, xcds)[0], (cus, xcds)
-    # C3 on MI355X keeps the tuned order: XCD-aware, a tail of 64 programs per XCD, half private
+    # C3 on MI355X keeps the tuned order: XCD-aware, a tail of 64 programs per XCD in one shared
+    # pool; a build with half of them private gives each XCD a queue of 32
     _, info = library_map(fn, (1, 32, 8, 8192, 128, 1, 1, 128, 256, 8, 0))
+    assert (info["static_blocks"], info["tail_wgs"], info["queues"], info["private"],
+            info["shared"]) == (1536, 640, 1, 0, 512)
+    _, info = library_map(fn, (1, 32, 8, 8192, 128, 1, 1, 128, 256, 8, 0), private_pct=50)
     assert (info["static_blocks"], info["tail_wgs"], info["queues"], info["private"],
             info["shared"]) == (1536, 640, 8, 32, 256)

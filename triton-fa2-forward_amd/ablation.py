@@ -19,6 +19,8 @@ never loads. The reference's variants (bench/ablation.py:1-20, 42-53):
   no_softmax       no mask, max, exp, sum or rescale        (output wrong on purpose)
   kv_l2            every tile loads K/V tile 0 again: L2 hits instead of HBM reads
   matmul_only      no_softmax + kv_l2: the two products and the loads' issue cost
+  no_kv_staging    K/V tiles from the third on are not loaded at all (output wrong on purpose;
+                   not in the reference): what staging K/V through LDS costs beyond the first tiles
   pack             copy with GQA head packing forced on
   static_order     copy without the dynamic tail of causal grids: workgroup b runs program b
                    (not in the reference; what the run-time dealing of the last programs buys)
@@ -53,7 +55,7 @@ ABLATE_LIB_PATH = os.path.join(HERE, "libfa2_ablate.so")
 
 # switch -> VARIANT bit (FA2_ABLATE_* in include/fa2_ablate.h)
 SWITCH_BITS = {"scale_first": 1, "mask_every_tile": 2, "no_exp": 8, "no_softmax": 16, "kv_l2": 32,
-               "static_order": 128}
+               "static_order": 128, "no_kv_staging": 256}
 KNOBS = tuple(SWITCH_BITS)
 VARIANTS = {
     "copy": (),
@@ -64,6 +66,7 @@ VARIANTS = {
     "no_softmax": ("no_softmax",),
     "kv_l2": ("kv_l2",),
     "matmul_only": ("no_softmax", "kv_l2"),
+    "no_kv_staging": ("no_kv_staging",),
     "pack": ("pack",),
     "static_order": ("static_order",),
 }

@@ -22,6 +22,7 @@ constexpr int kAblationVariants[] = {
     kVariantNoSoftmax,                            // no_softmax
     kVariantKvL2,                                 // kv_l2
     kVariantNoSoftmax | kVariantKvL2,             // matmul_only
+    kVariantNoKvStaging,                          // no_kv_staging (not in the reference)
     kVariantTimeline,                             // copy + per-workgroup timeline records
 };
 

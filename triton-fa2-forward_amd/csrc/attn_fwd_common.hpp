@@ -50,6 +50,9 @@ constexpr int kVariantKeyBound = 4;
 constexpr int kVariantNoExp = 8;       // exp2 replaced by its argument (alpha too)
 constexpr int kVariantNoSoftmax = 16;  // no mask, row max, exp, sum or rescale: O = (Q K^T) V
 constexpr int kVariantKvL2 = 32;       // every tile loads the first K/V tile again (L2 hits)
+// K/V tiles from the third on are not loaded: every tile's products read whichever of the first
+// two tiles its LDS buffer holds. What staging K/V through LDS costs beyond the first tiles.
+constexpr int kVariantNoKvStaging = 256;
 // Measurement library only, and computes the product's attention: every workgroup also records
 // its timeline (Params::timeline, kTimelineWords words); waits for its stores before the last stamp.
 constexpr int kVariantTimeline = 64;

@@ -138,11 +138,23 @@ int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim, const Topology
   return (int32_t)chunk;
 }
 
-// Share of each XCD's tail programs that its own workgroups take first (its queue), in percent;
-// the rest form the shared pool that any XCD takes from. Compile-time so that an A/B of two
-// builds can compare values (ab.py).
+// Tail policy knobs, compile-time so that an A/B of two builds can compare values (ab.py):
+//   FA2_TAIL_PRIVATE_PCT  share of each XCD's tail programs that its own workgroups take first
+//                         (its queue); the rest form the shared pool that any XCD takes from
+//   FA2_TAIL_SHARE_PCT    the tail's share of each XCD's programs (at most)
+//   FA2_TAIL_CHUNK_PCT    ... and of one unit chunk's programs (at most)
+//   FA2_TAIL_EXTRA_PCT    spare tail workgroups, in percent of the grid
 #ifndef FA2_TAIL_PRIVATE_PCT
-#define FA2_TAIL_PRIVATE_PCT 50
+#define FA2_TAIL_PRIVATE_PCT 0
+#endif
+#ifndef FA2_TAIL_SHARE_PCT
+#define FA2_TAIL_SHARE_PCT 25
+#endif
+#ifndef FA2_TAIL_CHUNK_PCT
+#define FA2_TAIL_CHUNK_PCT 50
+#endif
+#ifndef FA2_TAIL_EXTRA_PCT
+#define FA2_TAIL_EXTRA_PCT 6
 #endif
 
 // Dynamic tail of causal grids. Each XCD's programs run in a static order (program_of), but the
@@ -171,21 +183,22 @@ struct TailSchedule {
 };
 TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, int64_t progs_per_kv,
                            int64_t n_tiles, int32_t chunk, int head_dim, int bn,
-                           const Topology& topo) {
+                           const Topology& topo, int private_pct = FA2_TAIL_PRIVATE_PCT) {
   TailSchedule s;
   if (!causal || splits != 1 || waves != 4) return s;
   const int64_t xcds = int64_t(1) << topo.xcd_shift;
   // workgroups one XCD holds at once: its CUs x (3 at head_dim 64, 64-key tiles; else 2)
   const int64_t slots = std::max<int64_t>(1, topo.cus / xcds) * ((head_dim == 64 && bn <= 64) ? 3 : 2);
   const int64_t grid = units * progs_per_kv * n_tiles;
-  const int64_t extra = (grid * 6 / 100 + xcds - 1) / xcds * xcds;
+  const int64_t extra = (grid * FA2_TAIL_EXTRA_PCT / 100 + xcds - 1) / xcds * xcds;
   if (grid + extra > 0x7fffffffLL) return s;
   if (units % xcds) {
     // program_of's fallback order (q tile outermost, heaviest first; the hardware still deals
     // block b to XCD b % xcds): the last quarter of every XCD's blocks, and the remainder
     const int64_t per_xcd = grid / xcds;
     if (per_xcd < 2 * slots) return s;
-    const int64_t static_blocks = (per_xcd - (per_xcd + 3) / 4) * xcds;
+    const int64_t static_blocks =
+        (per_xcd - (per_xcd * FA2_TAIL_SHARE_PCT + 99) / 100) * xcds;
     s.static_blocks = (int32_t)static_blocks;
     s.shared = (int32_t)(grid - static_blocks);
     s.tail_wgs = (int32_t)(grid - static_blocks + extra);
@@ -195,9 +208,10 @@ TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, in
   const int64_t per_xcd = upx * progs_per_kv * n_tiles;
   if (per_xcd < 2 * slots) return s;
   const int64_t cu = (chunk > 0 && upx % chunk == 0) ? chunk : upx;  // program_of's chunk
-  const int64_t tail = std::min((per_xcd + 3) / 4, cu * progs_per_kv * n_tiles / 2);
+  const int64_t tail = std::min((per_xcd * FA2_TAIL_SHARE_PCT + 99) / 100,
+                                cu * progs_per_kv * n_tiles * FA2_TAIL_CHUNK_PCT / 100);
   if (tail < 1) return s;
-  const int64_t priv = tail * FA2_TAIL_PRIVATE_PCT / 100;
+  const int64_t priv = tail * private_pct / 100;
   s.static_blocks = (int32_t)((per_xcd - tail) * xcds);
   s.queues = xcds > 1 && priv > 0 ? (int32_t)xcds : 1;
   s.private_per_queue = s.queues > 1 ? (int32_t)priv : 0;
@@ -393,7 +407,8 @@ struct LaunchPlan {
 
 // Every check of a call (fa2/kernel.py:218-244 restated for a C caller) and its plan, on the
 // given topology. No device call: the measurement library runs it on the CPU as well.
-int plan_launch(const LaunchArgs& a, const Topology& topo, LaunchPlan* out) {
+int plan_launch(const LaunchArgs& a, const Topology& topo, LaunchPlan* out,
+                int tail_private_pct = FA2_TAIL_PRIVATE_PCT) {
   g_err[0] = '\0';
   LaunchPlan pl;
   // ---- shape checks (fa2/kernel.py:218-228)
@@ -564,7 +579,7 @@ int plan_launch(const LaunchArgs& a, const Topology& topo, LaunchPlan* out) {
   }
   if (!a.static_order)
     pl.tail = tail_schedule(a.causal != 0, splits, waves, n_bh / (group / a.pack), group / a.pack,
-                            n_tiles, p.unit_chunk, a.head_dim, bn, topo);
+                            n_tiles, p.unit_chunk, a.head_dim, bn, topo, tail_private_pct);
   if (pl.tail.tail_wgs > 0) grid = (int64_t)pl.tail.static_blocks + pl.tail.tail_wgs;
   pl.di = di;
   pl.waves = waves;

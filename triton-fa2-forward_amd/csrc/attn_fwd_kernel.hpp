@@ -62,8 +62,8 @@ __device__ __forceinline__ int take_tail_program(const Params& p, int block) {
 // kVariantScaleFirst scales every score before the row max and subtracts the max separately
 // (two VALU instructions per score instead of one FMA); kVariantMaskEveryTile applies the mask
 // on every K/V tile, not only on the tiles that need it (both still compute attention); and the
-// knockouts kVariantNoExp, kVariantNoSoftmax and kVariantKvL2, which skip work and compute
-// garbage on purpose (their time is the point). With none of these bits the code is unchanged.
+// knockouts kVariantNoExp, kVariantNoSoftmax, kVariantKvL2 and kVariantNoKvStaging, which skip
+// work and compute garbage on purpose (their time is the point). With none of these bits the code is unchanged.
 //
 // Register budget: two waves per SIMD (256 VGPRs each), except for the software-pipelined loop
 // (head_dim 64, 64- or 32-key tiles), which is held to three (168 VGPRs): measured +4.5-5.5% for
@@ -79,6 +79,7 @@ void attn_fwd_kernel(const Params p) {
   constexpr bool kNoExp = (VARIANT & kVariantNoExp) != 0;
   constexpr bool kNoSoftmax = (VARIANT & kVariantNoSoftmax) != 0;
   constexpr bool kKvL2 = (VARIANT & kVariantKvL2) != 0;
+  constexpr bool kNoKvStaging = (VARIANT & kVariantNoKvStaging) != 0;
   constexpr bool kTimeline = (VARIANT & kVariantTimeline) != 0;
   const uint64_t tl_entry = kTimeline ? __builtin_amdgcn_s_memrealtime() : 0;
   uint64_t tl_prologue = 0, tl_loop = 0;
@@ -233,6 +234,7 @@ void attn_fwd_kernel(const Params p) {
     return make_desc(base + (uint64_t)(uint32_t)n0 * stride2, bytes);
   };
   auto issue_k = [&](int n0, int buf) {
+    if (kNoKvStaging && n0 >= kv_begin + 2 * BN) return;
     const auto rs = rsrc_at(kbase, p.skn, kKvL2 ? kv_begin : n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
@@ -241,6 +243,7 @@ void attn_fwd_kernel(const Params p) {
     }
   };
   auto issue_v = [&](int n0, int buf) {
+    if (kNoKvStaging && n0 >= kv_begin + 2 * BN) return;
     const auto rs = rsrc_at(vbase, p.svn, kKvL2 ? kv_begin : n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {

@@ -15,6 +15,11 @@ its own C-ABI file fa2_ablate.hip into triton-fa2-forward_amd/libfa2_ablate.so, 
 fa2 package: the product never loads it. It also holds the MFMA ceiling probe (mfma_ceiling.hip):
 what the matrix cores sustain under the chip's power limit.
 
+`--variant NAME -D MACRO=VALUE ...` builds only the product library, with those compile-time
+definitions, into triton-fa2-forward_amd/variants/NAME/libfa2_fwd.so (objects under build/): a
+second build of the same sources for a same-box A/B against the product (ab.py), e.g. another
+FA2_TAIL_PRIVATE_PCT. It never replaces the product library.
+
 Both libraries are built with hidden visibility, so each exports exactly the functions its
 header declares (FA2_API). The compiler's resource report for every kernel instance (VGPRs,
 AGPRs, SGPRs, spills, LDS, occupancy; -Rpass-analysis=kernel-resource-usage) is saved to
@@ -104,6 +109,40 @@ def describe_instance(name):
             "block_n": bn, "causal": bool(causal), "variant": variant}
 
 
+VARIANTS_DIR = os.path.join(PKG, "variants")
+
+
+def build_variant(name, defines, jobs=8, verbose=False):
+    """The product library compiled with extra -D definitions, linked to
+    variants/NAME/libfa2_fwd.so. Returns its path."""
+    if not re.fullmatch(r"[A-Za-z0-9_.-]+", name):
+        raise ValueError(f"variant name {name!r}: letters, digits, '_', '.', '-' only")
+    obj_dir = os.path.join(PKG, "build", "variants", name)
+    out_dir = os.path.join(VARIANTS_DIR, name)
+    os.makedirs(obj_dir, exist_ok=True)
+    os.makedirs(out_dir, exist_ok=True)
+    cc = hipcc()
+    flags = [*common_flags(), *(f"-D{d}" for d in defines)]
+    cmds = []
+    for dt in DTYPES:
+        for d in HEAD_DIMS:
+            cmds.append([cc, *flags, f"-DFA2_DT={dt}", f"-DFA2_D={d}", "-c",
+                         os.path.join(CSRC, "attn_fwd_inst.hip"), "-o",
+                         os.path.join(obj_dir, f"attn_fwd_dt{dt}_d{d}.o")])
+    for name_ in ("attn_fwd_combine", "attn_key_norm", "fa2_fwd", "fa2_scratch"):
+        cmds.append([cc, *flags, "-c", os.path.join(CSRC, name_ + ".hip"), "-o",
+                     os.path.join(obj_dir, name_ + ".o")])
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(lambda cmd: _run(cmd, verbose), cmds))
+    path = os.path.join(out_dir, "libfa2_fwd.so")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", path + ".tmp",
+          *(c[-1] for c in cmds)], verbose)
+    os.replace(path + ".tmp", path)
+    with open(os.path.join(out_dir, "defines.txt"), "w") as f:
+        f.write("\n".join(defines) + "\n")
+    return path
+
+
 def build(jobs=8, verbose=False):
     """Compile every kernel instance and link both libraries. Returns the product .so path."""
     os.makedirs(OBJ_DIR, exist_ok=True)
@@ -174,8 +213,16 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("-j", "--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--variant", default=None, help="build only the product library, with -D, "
+                    "into variants/VARIANT/libfa2_fwd.so")
+    ap.add_argument("-D", dest="defines", action="append", default=[], metavar="MACRO=VALUE")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    if args.variant:
+        print(build_variant(args.variant, args.defines, args.jobs, args.verbose))
+    elif args.defines:
+        ap.error("-D needs --variant (the product library is always built as shipped)")
+    else:
+        print(build(args.jobs, args.verbose))
 
 
 if __name__ == "__main__":

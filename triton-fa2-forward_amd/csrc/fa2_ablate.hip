@@ -32,7 +32,7 @@ int launch_ablate(int dtype, int di, const Params& p, int waves, int block_n, bo
 // tile, without a workspace (no split-KV, no key-norm table), on `topo`. No device call.
 int plan_default(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t head_dim,
                  int32_t causal, int32_t pack, int32_t block_m, const Topology& topo,
-                 bool static_order, LaunchPlan* pl) {
+                 bool static_order, LaunchPlan* pl, int private_pct = FA2_TAIL_PRIVATE_PCT) {
   if (batch < 1 || h_q < 1 || h_kv < 1 || n_q < 1 || h_q % h_kv)
     return fail(FA2_EINVAL, "bad sizes: batch=%d h_q=%d h_kv=%d n_q=%d", batch, h_q, h_kv, n_q);
   const int64_t d = head_dim;
@@ -43,7 +43,7 @@ int plan_default(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q, int32_t 
   const LaunchArgs a{fake, fake, fake, fake, sq, sk, sk, sq, batch, h_q, h_kv, n_q, n_q,
                      head_dim, FA2_DTYPE_BF16, causal, pack, block_m, 0, 1.0f, nullptr, 1,
                      nullptr, 0, 0, nullptr, 0, static_order};
-  return plan_launch(a, topo, pl);
+  return plan_launch(a, topo, pl, private_pct);
 }
 
 }  // namespace
@@ -108,16 +108,19 @@ int fa2_ablate_tail_schedule(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n
 
 int fa2_ablate_program_map(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
                            int32_t head_dim, int32_t causal, int32_t pack, int32_t block_m,
-                           int32_t cus, int32_t xcds, int32_t static_order, uint32_t seed,
-                           int32_t* programs, int64_t program_words, int32_t* info,
-                           int32_t info_words) {
+                           int32_t cus, int32_t xcds, int32_t static_order,
+                           int32_t tail_private_pct, uint32_t seed, int32_t* programs,
+                           int64_t program_words, int32_t* info, int32_t info_words) {
   g_err[0] = '\0';
   if (!programs || !info || info_words < FA2_ABLATE_MAP_INFO_WORDS)
     return fail(FA2_EINVAL, "null output or info shorter than %d words", FA2_ABLATE_MAP_INFO_WORDS);
   if (cus < 1 || xcds < 1) return fail(FA2_EINVAL, "cus and xcds must be positive");
+  if (tail_private_pct < -1 || tail_private_pct > 100)
+    return fail(FA2_EINVAL, "tail_private_pct must be -1 (the library's) or in [0, 100]");
   LaunchPlan pl;
   const int rc = plan_default(batch, h_q, h_kv, n_q, head_dim, causal, pack, block_m,
-                              make_topology(cus, xcds), static_order != 0, &pl);
+                              make_topology(cus, xcds), static_order != 0, &pl,
+                              tail_private_pct < 0 ? FA2_TAIL_PRIVATE_PCT : tail_private_pct);
   if (rc != FA2_OK) return rc;
   const int64_t grid = pl.empty ? 0 : pl.grid;
   if (program_words < 3 * grid)

@@ -8,6 +8,9 @@ bench/profile_target.py).
 --pack-short N_Q runs the reference's few-queries shape instead (bench.py --pack-short: fp16,
 B 16, H 32/8, N_kv 4096, D 128, non-causal, default path: packed, automatic split-KV).
 
+--lib PATH runs another build of the product library (csrc/build.py --variant) through the same
+call attention() makes (ab.py's), for the counters of an A/B.
+
 --copy-mib adds one plain device-to-device copy of that many MiB after the attention launches.
 Its FETCH_SIZE / WRITE_SIZE reading, against the bytes it is known to move, is the scale factor
 that turns the counters' KiB into bytes for the attention kernel.
@@ -30,6 +33,7 @@ def main():
     ap.add_argument("--block-m", type=int, default=None)
     ap.add_argument("--block-n", type=int, default=None)
     ap.add_argument("--pack-short", type=int, default=None, metavar="N_Q")
+    ap.add_argument("--lib", default=None, help="another build of libfa2_fwd.so (ab.py's call)")
     args = ap.parse_args()
 
     import torch
@@ -48,8 +52,17 @@ def main():
     else:
         q, k, v, causal = bench.make_inputs(args.config, "cuda")
         print(f"profile_target: {bench.describe(args.config)}, {args.launches} launches", flush=True)
+    if args.lib:
+        import ab
+
+        out = torch.empty_like(q)
+        call = ab.make_call(ab.load(args.lib), q, k, v, out, causal, True)
+        print(f"profile_target: library {args.lib}", flush=True)
+    else:
+        call = lambda: attention(q, k, v, causal=causal, block_m=args.block_m,  # noqa: E731
+                                 block_n=args.block_n)
     for _ in range(args.launches):
-        attention(q, k, v, causal=causal, block_m=args.block_m, block_n=args.block_n)
+        call()
     torch.cuda.synchronize()
     if args.copy_mib:
         n = args.copy_mib << 20
