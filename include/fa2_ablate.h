@@ -37,6 +37,14 @@ extern "C" {
  * whichever of the first two tiles its LDS buffer holds; output wrong on purpose): what the
  * HBM/L2 -> LDS staging of K/V costs beyond the first tiles. */
 #define FA2_ABLATE_NO_KV_STAGING 256
+/* Not in the reference: each workgroup runs its program with 8 waves in two groups of 4 on the
+ * same 128 rows, group 0 over the first half of the key range and group 1 over the rest, each
+ * with K/V buffers of its own (128 KiB of LDS: one workgroup per CU), and merges the two partial
+ * softmax states through LDS before one store. Still attention (another summation order, so
+ * not the product's bits); head_dim 128 only (FA2_EINVAL otherwise); always the static order.
+ * What halving the longest program's key range buys against losing the second workgroup per
+ * CU. */
+#define FA2_ABLATE_SPLIT_KEYS 512
 /* Not a kernel switch and not in the reference: the launch keeps the static order of programs
  * (workgroup b runs program b) where fa2_attn_fwd deals a causal grid's last programs at run
  * time (its dynamic tail). Combines with any variant; the output is the same bit for bit. */
@@ -56,6 +64,7 @@ extern "C" {
  *              FA2_ABLATE_KV_L2                           kv_l2
  *              FA2_ABLATE_NO_SOFTMAX | FA2_ABLATE_KV_L2   matmul_only
  *              FA2_ABLATE_NO_KV_STAGING                   no_kv_staging (not in the reference)
+ *              FA2_ABLATE_SPLIT_KEYS                      split_keys (not in the reference)
  *            each optionally with FA2_ABLATE_STATIC_ORDER;
  *            other bit sets are rejected (FA2_EINVAL).
  * The other arguments are fa2_attn_fwd's (include/fa2_fwd.h), with the same checks. Runs at the

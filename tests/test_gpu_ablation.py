@@ -7,6 +7,9 @@ reference tests its knockout copy (tests/test_ablation.py:16-48):
 * mask_every_tile only adds work: still bit for bit;
 * scale_first, and both switches together (the reference's "before_fixes"), still compute
   attention: the 2x-SDPA rule against the fp64 oracle;
+* the key split (8 waves in two groups over the halves of each program's key range, merged
+  through LDS) is still attention: the 2x-SDPA rule against the fp64 oracle on ragged, GQA,
+  causal and full shapes, and C5 at full size against the fp32 oracle;
 * the work-skipping knockouts (no_exp, no_softmax, kv_l2, matmul_only, no_kv_staging) change the output
   (tests/test_ablation.py:28-34), on both of the kernel's tile loops (software-pipelined at
   head_dim 64, one tile at a time otherwise), causal or not.
@@ -200,3 +203,35 @@ def test_hbm_read_probe_reads_every_word():
         for w in out.cpu().tolist():
             got ^= w & 0xFFFFFFFF
         assert got == want, wg
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 8, 2, 300), (1, 4, 4, 64), (1, 4, 4, 65), (2, 8, 8, 1000),
+                                   (1, 7, 1, 129)])
+def test_split_keys_is_attention(shape, dtype, causal):
+    """One tile (group 1 idle), 65 keys (group 1 one masked tile), odd tile counts (group 1 one
+    tile fewer), rows whose keys all lie in group 0's half (causal), GQA."""
+    B, hq, hkv, N = shape
+    print(f"split_keys: B={B} Hq={hq} Hkv={hkv} N={N} {dtype} causal={causal}", flush=True)
+    q, k, v = make_qkv(B, hq, hkv, N, N, 128, dtype)
+    out = _ablate()(q, k, v, causal=causal, split_keys=True)
+    check_against_oracle(q, k, v, causal, ours=out)
+
+
+def test_split_keys_on_c5_meets_the_fp32_oracle():
+    import bench
+
+    q, k, v, causal = bench.make_inputs("C5", "cuda")
+    print("split_keys: C5 full size", flush=True)
+    out = _ablate()(q, k, v, causal=causal, split_keys=True)
+    check_against_oracle(q, k, v, causal, precision=torch.float32, ours=out)
+    again = _ablate()(q, k, v, causal=causal, split_keys=True)
+    assert torch.equal(out, again)
+
+
+def test_split_keys_needs_head_dim_128():
+    q, k, v = make_qkv(1, 4, 4, 64, 64, 64, torch.float16)
+    with pytest.raises(RuntimeError):
+        _ablate()(q, k, v, causal=True, split_keys=True)
+        torch.cuda.synchronize()

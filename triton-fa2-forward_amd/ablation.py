@@ -21,6 +21,9 @@ never loads. The reference's variants (bench/ablation.py:1-20, 42-53):
   matmul_only      no_softmax + kv_l2: the two products and the loads' issue cost
   no_kv_staging    K/V tiles from the third on are not loaded at all (output wrong on purpose;
                    not in the reference): what staging K/V through LDS costs beyond the first tiles
+  split_keys       8 waves per program in two groups over the two halves of its key range,
+                   merged through LDS, one workgroup per CU (head_dim 128; still attention; not in
+                   the reference): what halving the longest program's path buys
   pack             copy with GQA head packing forced on
   static_order     copy without the dynamic tail of causal grids: workgroup b runs program b
                    (not in the reference; what the run-time dealing of the last programs buys)
@@ -55,7 +58,7 @@ ABLATE_LIB_PATH = os.path.join(HERE, "libfa2_ablate.so")
 
 # switch -> VARIANT bit (FA2_ABLATE_* in include/fa2_ablate.h)
 SWITCH_BITS = {"scale_first": 1, "mask_every_tile": 2, "no_exp": 8, "no_softmax": 16, "kv_l2": 32,
-               "static_order": 128, "no_kv_staging": 256}
+               "static_order": 128, "no_kv_staging": 256, "split_keys": 512}
 KNOBS = tuple(SWITCH_BITS)
 VARIANTS = {
     "copy": (),
@@ -67,6 +70,7 @@ VARIANTS = {
     "kv_l2": ("kv_l2",),
     "matmul_only": ("no_softmax", "kv_l2"),
     "no_kv_staging": ("no_kv_staging",),
+    "split_keys": ("split_keys",),
     "pack": ("pack",),
     "static_order": ("static_order",),
 }

@@ -23,6 +23,7 @@ constexpr int kAblationVariants[] = {
     kVariantKvL2,                                 // kv_l2
     kVariantNoSoftmax | kVariantKvL2,             // matmul_only
     kVariantNoKvStaging,                          // no_kv_staging (not in the reference)
+    kVariantSplitKeys,                            // split_keys (not in the reference)
     kVariantTimeline,                             // copy + per-workgroup timeline records
 };
 

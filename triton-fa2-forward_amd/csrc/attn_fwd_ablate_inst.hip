@@ -15,13 +15,28 @@ namespace {
 template <int DT, int D, int VARIANT>
 int launch_variant(const Params& p, bool causal, unsigned grid, hipStream_t s) {
   constexpr int BN = default_block_n(D);
-  if (causal)
-    hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, VARIANT>), dim3(grid), dim3(256), 0,
-                       s, p);
-  else
-    hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, VARIANT>), dim3(grid), dim3(256), 0,
-                       s, p);
-  return (int)hipGetLastError();
+  if constexpr ((VARIANT & kVariantSplitKeys) != 0) {
+    // the key split: 8 waves, two groups of 4 on the same 128 rows; head_dim 128 only
+    if constexpr (D != 128) {
+      return (int)hipErrorInvalidValue;
+    } else {
+      if (causal)
+        hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 8, BN, true, VARIANT>), dim3(grid), dim3(512),
+                           0, s, p);
+      else
+        hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 8, BN, false, VARIANT>), dim3(grid), dim3(512),
+                           0, s, p);
+      return (int)hipGetLastError();
+    }
+  } else {
+    if (causal)
+      hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, VARIANT>), dim3(grid), dim3(256), 0,
+                         s, p);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, VARIANT>), dim3(grid), dim3(256),
+                         0, s, p);
+    return (int)hipGetLastError();
+  }
 }
 
 template <int DT, int D, int... V>
@@ -39,11 +54,11 @@ int launch_attn_fwd_ablate(const Params& p, int variant, bool causal, unsigned g
   return dispatch<DT, D, kAblationVariants[0], kAblationVariants[1], kAblationVariants[2],
                   kAblationVariants[3], kAblationVariants[4], kAblationVariants[5],
                   kAblationVariants[6], kAblationVariants[7], kAblationVariants[8],
-                  kAblationVariants[9]>(
+                  kAblationVariants[9], kAblationVariants[10]>(
       p, variant, causal, grid, s);
 }
 
-static_assert(sizeof(kAblationVariants) / sizeof(int) == 10, "dispatch lists every variant");
+static_assert(sizeof(kAblationVariants) / sizeof(int) == 11, "dispatch lists every variant");
 
 template int launch_attn_fwd_ablate<FA2_DT, FA2_D>(const Params&, int, bool, unsigned,
                                                    hipStream_t);

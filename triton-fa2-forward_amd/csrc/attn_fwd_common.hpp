@@ -53,6 +53,10 @@ constexpr int kVariantKvL2 = 32;       // every tile loads the first K/V tile ag
 // K/V tiles from the third on are not loaded: every tile's products read whichever of the first
 // two tiles its LDS buffer holds. What staging K/V through LDS costs beyond the first tiles.
 constexpr int kVariantNoKvStaging = 256;
+// Measurement library only, and computes attention (in another summation order): twice the waves
+// per workgroup, in two groups that take the two halves of each program's key range with K/V
+// buffers of their own, and merge through LDS (one workgroup per CU).
+constexpr int kVariantSplitKeys = 512;
 // Measurement library only, and computes the product's attention: every workgroup also records
 // its timeline (Params::timeline, kTimelineWords words); waits for its stores before the last stamp.
 constexpr int kVariantTimeline = 64;

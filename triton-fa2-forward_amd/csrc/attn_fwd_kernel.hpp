@@ -81,6 +81,15 @@ void attn_fwd_kernel(const Params p) {
   constexpr bool kKvL2 = (VARIANT & kVariantKvL2) != 0;
   constexpr bool kNoKvStaging = (VARIANT & kVariantNoKvStaging) != 0;
   constexpr bool kTimeline = (VARIANT & kVariantTimeline) != 0;
+  // Measurement library only: the workgroup's waves form two groups of NW / 2 that run the same
+  // rows over the two halves of the program's key range, each group with K/V buffers of its own,
+  // and merge (m, l, O) through LDS before one store (one workgroup per CU).
+  constexpr bool kSplit = (VARIANT & kVariantSplitKeys) != 0;
+  constexpr int KG = kSplit ? 2 : 1;       // key groups
+  constexpr int GW = NW / KG;              // waves per key group
+  static_assert(!kSplit || !(D == 64 && BN <= 64), "the key split runs the one-tile loop");
+  static_assert(!kSplit || (VARIANT & (kVariantKeyBound | kVariantTimeline)) == 0,
+                "the key split has no key-norm bound and no timeline");
   const uint64_t tl_entry = kTimeline ? __builtin_amdgcn_s_memrealtime() : 0;
   uint64_t tl_prologue = 0, tl_loop = 0;
   // exp2, or (knockout) its argument
@@ -93,14 +102,16 @@ void attn_fwd_kernel(const Params p) {
   constexpr int NI = TCH / 64;             // 64-lane LDS load instructions per tile
   static_assert(TCH % 64 == 0, "a tile must be whole 1 KiB load instructions");
 
-  __shared__ u32x4 k_lds[2][TCH];
-  __shared__ u32x4 v_lds[2][TCH];
+  __shared__ u32x4 k_lds[KG][2][TCH];
+  __shared__ u32x4 v_lds[KG][2][TCH];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS addresses stay scalar
   const int lane = tid & 63;
   const int c = lane & 31;
   const int g = lane >> 5;
+  const int grp = kSplit ? wave / GW : 0;  // key group (uniform)
+  const int gwave = wave - grp * GW;        // wave inside its group: 32 rows each
 
   // split-KV: consecutive workgroups are the splits of one program
   const int split = p.splits > 1 ? (int)blockIdx.x % p.splits : 0;
@@ -120,7 +131,7 @@ void attn_fwd_kernel(const Params p) {
   // ---- this lane's query row: packed row r -> (position r / pack, head r % pack)
   // (fa2/kernel.py:135-139). Rows past block_m or past n_q compute on zeros and are
   // never stored; they see every key so their softmax stays finite.
-  const int lrow = wave * 32 + c;
+  const int lrow = gwave * 32 + c;
   const int r = pr.tile * p.block_m + lrow;
   const int pos = r / p.pack;
   const int head = pr.hq0 + (r - pos * p.pack);
@@ -153,7 +164,21 @@ void attn_fwd_kernel(const Params p) {
       kv_end = min(kv_begin + p.split_tiles * BN, p.n_kv);
     }
   }
-  const int n_tiles_kv = (kv_end - kv_begin + BN - 1) / BN;
+  int n_tiles_kv = (kv_end - kv_begin + BN - 1) / BN;
+  // key groups: the first ceil(n / 2) tiles to group 0, the rest to group 1; both groups run
+  // n_iter trips of the tile loop, one barrier each (a group with fewer tiles idles through them)
+  int n_iter = n_tiles_kv;
+  if constexpr (kSplit) {
+    const int h = (n_tiles_kv + 1) / 2;
+    n_iter = h;
+    if (grp == 0) {
+      kv_end = min(kv_begin + h * BN, kv_end);
+      n_tiles_kv = h;
+    } else {
+      kv_begin += h * BN;
+      n_tiles_kv -= h;
+    }
+  }
 
   // ---- score bound from the key-norm table (fa2_attn_fwd_ex with a workspace): a row's scores
   // obey |q . k| <= |q| max|k| over the keys it sees. A causal row sees keys [0, pos]: the chunks
@@ -211,13 +236,13 @@ void attn_fwd_kernel(const Params p) {
   // (16 bytes, P = 64 * instruction + lane) holds row P / CPR, logical chunk
   // (P % CPR) ^ key(row). The per-lane byte offsets are fixed; each tile moves the base of a
   // buffer resource that ends after row n_kv - 1, so rows past the sequence read as zeros.
-  constexpr int JW = (NI + NW - 1) / NW;  // load instructions per wave per tensor
+  constexpr int JW = (NI + GW - 1) / GW;  // load instructions per wave per tensor
   const char* kbase = (const char*)(p.k + pr.b * p.skb + pr.hkv * p.skh);
   const char* vbase = (const char*)(p.v + pr.b * p.svb + pr.hkv * p.svh);
   uint32_t koff[JW], voff[JW];
 #pragma unroll
   for (int jj = 0; jj < JW; ++jj) {
-    const int P = (wave + jj * NW) * 64 + lane;
+    const int P = (gwave + jj * GW) * 64 + lane;
     const int row = P / CPR, col = P % CPR;
     koff[jj] = (uint32_t)(row * p.skn + (col ^ k_key<D>(pi_row(row & 31) & 15)) * 8) * 2u;
     voff[jj] = (uint32_t)(row * p.svn + (col ^ v_key<D>(row & 15)) * 8) * 2u;
@@ -238,8 +263,8 @@ void attn_fwd_kernel(const Params p) {
     const auto rs = rsrc_at(kbase, p.skn, kKvL2 ? kv_begin : n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
-      const int j = wave + jj * NW;
-      if (NI % NW == 0 || j < NI) load_lds16(rs, koff[jj], lds_addr((const FA2_LDS char*)k_lds[buf] + j * 64 * 16));
+      const int j = gwave + jj * GW;
+      if (NI % GW == 0 || j < NI) load_lds16(rs, koff[jj], lds_addr((const FA2_LDS char*)k_lds[grp][buf] + j * 64 * 16));
     }
   };
   auto issue_v = [&](int n0, int buf) {
@@ -247,8 +272,8 @@ void attn_fwd_kernel(const Params p) {
     const auto rs = rsrc_at(vbase, p.svn, kKvL2 ? kv_begin : n0);
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj) {
-      const int j = wave + jj * NW;
-      if (NI % NW == 0 || j < NI) load_lds16(rs, voff[jj], lds_addr((const FA2_LDS char*)v_lds[buf] + j * 64 * 16));
+      const int j = gwave + jj * GW;
+      if (NI % GW == 0 || j < NI) load_lds16(rs, voff[jj], lds_addr((const FA2_LDS char*)v_lds[grp][buf] + j * 64 * 16));
     }
   };
 
@@ -282,18 +307,18 @@ void attn_fwd_kernel(const Params p) {
     }
   // A operand of S^T: 32 keys (rows pi(c) of key block nb) x 16 dims (k-step ks)
   auto k_operand = [&](int buf, int ks, int nb) {
-    const char FA2_LDS* kt = (const char FA2_LDS*)k_lds[buf] + koffs[ks];
+    const char FA2_LDS* kt = (const char FA2_LDS*)k_lds[grp][buf] + koffs[ks];
     return *(const u32x4 FA2_LDS*)(kt + nb * 32 * CPR * 16);
   };
   // The same read, volatile: used before the loop so that the compiler cannot merge it with
   // the in-loop prefetch into one load at the top of the loop (which would expose its latency).
   auto k_operand_v = [&](int buf, int ks, int nb) {
-    const char FA2_LDS* kt = (const char FA2_LDS*)k_lds[buf] + koffs[ks];
+    const char FA2_LDS* kt = (const char FA2_LDS*)k_lds[grp][buf] + koffs[ks];
     return *(const volatile u32x4 FA2_LDS*)(kt + nb * 32 * CPR * 16);
   };
   // A operand of O^T: 32 dims (block db) x 16 keys (k-step t), two transposing reads
   auto v_operand = [&](int buf, int t, int db) {
-    const char FA2_LDS* vt = (const char FA2_LDS*)v_lds[buf];
+    const char FA2_LDS* vt = (const char FA2_LDS*)v_lds[grp][buf];
     const u32x2 lo = lds_read_tr(vt + voffs[0][db] + t * 16 * D * 2);
     const u32x2 hi = lds_read_tr(vt + voffs[1][db] + t * 16 * D * 2);
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
@@ -339,16 +364,19 @@ void attn_fwd_kernel(const Params p) {
     constexpr int LA_V = NPV < kLaV ? NPV : kLaV;
     constexpr int NKP = LA_S * NB;               // K operand reads prefetched during PV
     u32x4 kop[LA_S][NB];
-    if (n_tiles_kv > 0) {
-      issue_k(kv_begin, 0);
-      issue_v(kv_begin, 0);
+    if (n_iter > 0) {
+      if (n_tiles_kv > 0) {
+        issue_k(kv_begin, 0);
+        issue_v(kv_begin, 0);
+      }
       if (n_tiles_kv > 1) issue_k(kv_begin + BN, 1);
       // S_0 needs Q and K_0 only: V_0 and K_1 (this wave's last loads; vector loads complete in
       // order) land while S_0 runs, and the loop's first wait covers them. When the waves issue
       // unequal numbers of loads, or more than the 6-bit counter holds, wait for all.
-      if constexpr (NI % NW == 0 && 2 * JW < 64) {
+      if constexpr (NI % GW == 0 && 2 * JW < 64) {
         if (n_tiles_kv > 1) wait_vmcnt<2 * JW>();
-        else wait_vmcnt<JW>();
+        else if (!kSplit || n_tiles_kv > 0) wait_vmcnt<JW>();
+        else wait_vmcnt<0>();
       } else {
         wait_vmcnt<0>();
       }
@@ -367,7 +395,8 @@ void attn_fwd_kernel(const Params p) {
     int n_active = n_tiles_kv;
     if (CAUSAL) {
       const int wave_last = __builtin_amdgcn_readlane(pos_vis, 31);  // rows grow with the lane
-      if (wave_last < kv_end) n_active = min(n_tiles_kv, (wave_last - kv_begin) / BN + 1);
+      if (kSplit && wave_last < kv_begin) n_active = 0;  // group 1: every key is past its rows
+      else if (wave_last < kv_end) n_active = min(n_tiles_kv, (wave_last - kv_begin) / BN + 1);
     }
     for (int j = 0; j < n_active; ++j) {
       const int n0 = kv_begin + j * BN;
@@ -447,11 +476,14 @@ void attn_fwd_kernel(const Params p) {
         }
       }
       if constexpr (!kNoSoftmax) {
+        // group 1 of the key split can meet rows with no visible key yet (reference -inf): their
+        // scores are all -inf, and a reference of 0 gives them weight 0 instead of NaN
+        const float m_ref = (kSplit && m_i == -INFINITY) ? 0.f : m_i;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
           for (int i = 0; i < 16; ++i)
-            s[nb][i] = ex2(kScaleFirst ? s[nb][i] - m_i : __builtin_fmaf(s[nb][i], qk_scale, -m_i));
+            s[nb][i] = ex2(kScaleFirst ? s[nb][i] - m_ref : __builtin_fmaf(s[nb][i], qk_scale, -m_ref));
         if constexpr (!kRoundedSum) {
           l_i += lane_sum(s);
         } else if (want_exact) {
@@ -500,7 +532,7 @@ void attn_fwd_kernel(const Params p) {
       }
     }
 
-    for (int j = n_active; j < n_tiles_kv; ++j) {
+    for (int j = n_active; j < n_iter; ++j) {
       const int n0 = kv_begin + j * BN;
       wait_vmcnt<0>();
       __syncthreads();
@@ -743,6 +775,40 @@ void attn_fwd_kernel(const Params p) {
 #pragma unroll
       for (int i = 0; i < LA_V; ++i) va[i] = v_operand(bufv, i / DB, i % DB);
       pv_product(pb, bufv, va);
+    }
+  }
+
+  // ---- key split: group 1 hands its (m, l, O) to group 0 through LDS, lane for lane (the two
+  // groups' waves hold the same rows in the same lanes); group 0 merges and stores
+  if constexpr (kSplit) {
+    static_assert(GW * DB * 16 * 64 * sizeof(float) <= sizeof(k_lds), "O fits the K buffers");
+    static_assert(GW * 3 * 64 * sizeof(float) <= sizeof(v_lds), "m, l fit the V buffers");
+    __syncthreads();  // every wave is done with every K/V buffer
+    float FA2_LDS* ob = (float FA2_LDS*)&k_lds[0][0][0];  // [GW][DB][16][64 lanes]
+    float FA2_LDS* sb = (float FA2_LDS*)&v_lds[0][0][0];  // [GW][3][64 lanes]
+    if (grp == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ob[((gwave * DB + db) * 16 + i) * 64 + lane] = acc[db][i];
+      sb[(gwave * 3 + 0) * 64 + lane] = m_i;
+      sb[(gwave * 3 + 1) * 64 + lane] = l_i;
+      sb[(gwave * 3 + 2) * 64 + lane] = l_exact;
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float mb = sb[(gwave * 3 + 0) * 64 + lane];
+    const float m_new = fmaxf(m_i, mb);
+    if (m_new != -INFINITY) {  // (no key at all: nothing to merge)
+      const float a = ex2(m_i - m_new), b = ex2(mb - m_new);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          acc[db][i] = acc[db][i] * a + ob[((gwave * DB + db) * 16 + i) * 64 + lane] * b;
+      l_i = l_i * a + sb[(gwave * 3 + 1) * 64 + lane] * b;
+      l_exact = l_exact * a + sb[(gwave * 3 + 2) * 64 + lane] * b;
+      m_i = m_new;
     }
   }
 

@@ -58,8 +58,10 @@ int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
                         int32_t h_q, int32_t h_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
                         int32_t dtype, int32_t causal, int32_t pack, float qk_scale,
                         int32_t variant, void* stream) {
-  // FA2_ABLATE_STATIC_ORDER is the host's: the launch keeps the static order (no dynamic tail)
-  const bool static_order = (variant & FA2_ABLATE_STATIC_ORDER) != 0;
+  // FA2_ABLATE_STATIC_ORDER is the host's: the launch keeps the static order (no dynamic tail);
+  // the key split always does (its workgroups hold a whole CU, which the tail's slots do not model)
+  const bool static_order =
+      (variant & FA2_ABLATE_STATIC_ORDER) != 0 || (variant & fa2::kVariantSplitKeys) != 0;
   variant &= ~FA2_ABLATE_STATIC_ORDER;
   // the timeline instance writes its records: only fa2_ablate_timeline, with a buffer, runs it
   if (!fa2::ablation_variant_built(variant) || (variant & fa2::kVariantTimeline)) {
