@@ -17,9 +17,13 @@ library runs W warmups and K launches back to back between one pair of HIP event
 drift within a round hits all libraries alike. The reference interleaves its variants the same
 way (bench/ablation.py:252-255).
 
-Workloads: the BASELINE configs by name (C2..C5), or X:B:Hq:Hkv:N:D:causal:dtype for any other
-shape (q, k, v from a CPU generator with seed 0); a ":nt" suffix gives no workspace (no key-norm
-table). Prints one line of JSON per workload, and a table.
+Workloads: the BASELINE configs by name (C2..C5), or X:B:Hq:Hkv:N:D:causal:dtype[:scale] for any
+other shape (q, k, v from a CPU generator with seed 0, times scale); a ":nt" suffix gives no
+workspace (no key-norm table), a ":kt" suffix a workspace with room for the table whatever the
+library's policy says (the table then always runs). A library given as NAME=PATH@kt or @nt
+takes that table mode on every workload, so that one build can be timed with and without the
+table in the same rounds (outputs then need not be equal bit for bit: rows that skip the row max
+round differently). Prints one line of JSON per workload, and a table.
 """
 
 import argparse
@@ -48,18 +52,24 @@ def load(path):
 
 
 def make_workload(spec):
-    """(q, k, v, causal, table) for a config name or X:B:Hq:Hkv:N:D:causal:dtype (+ ':nt')."""
+    """(q, k, v, causal, table) for a config name or X:B:Hq:Hkv:N:D:causal:dtype[:scale], with an
+    optional ':nt' (table False: no workspace) or ':kt' (table "force") suffix."""
     import torch
 
     import bench
 
-    table = not spec.endswith(":nt")
-    base = spec[:-3] if not table else spec
+    table = True
+    if spec.endswith(":nt") or spec.endswith(":kt"):
+        table = False if spec.endswith(":nt") else "force"
+        spec = spec[:-3]
+    base = spec
     if base.startswith("X:"):
-        _, B, hq, hkv, n, d, c, dt = base.split(":")
+        f = base.split(":")
+        B, hq, hkv, n, d, c, dt = f[1:8]
+        scale = float(f[8]) if len(f) > 8 else 1.0
         g = torch.Generator(device="cpu").manual_seed(0)
         dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dt]
-        q, k, v = (torch.randn(int(B), int(h), int(n), int(d), generator=g).to(dtype).cuda()
+        q, k, v = ((torch.randn(int(B), int(h), int(n), int(d), generator=g) * scale).to(dtype).cuda()
                    for h in (hq, hkv, hkv))
         return q, k, v, c == "1", table
     q, k, v, causal = bench.make_inputs(base, "cuda")
@@ -75,7 +85,10 @@ def make_call(h, q, k, v, out, causal, table):
     B, Hq, Nq, D = q.shape
     Hkv, Nkv = k.shape[1], k.shape[2]
     dt = _lib.DTYPE_CODE[q.dtype]
-    nb = h.fa2_workspace_bytes_for(B, Hq, Hkv, Nq, Nkv, D, dt, int(causal), 1) if table else 0
+    if table == "force":   # room for the key-norm table: one float per (batch, kv head, 64 keys)
+        nb = (B * Hkv * ((Nkv + 63) // 64) * 4 + 255) // 256 * 256
+    else:
+        nb = h.fa2_workspace_bytes_for(B, Hq, Hkv, Nq, Nkv, D, dt, int(causal), 1) if table else 0
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
     strides = [_lib._strides(t) for t in (q, k, v, out)]
     scale = 1.4426950408889634 / math.sqrt(D)
@@ -100,7 +113,8 @@ def ab(libs, spec, rounds, steps, warmup):
     B, Hq, N, D = q.shape
     flops = bench.attn_flops(B, Hq, N, k.shape[2], D, causal)
     outs = {n: torch.empty_like(q) for n in libs}
-    fns = {n: make_call(h, q, k, v, outs[n], causal, table) for n, h in libs.items()}
+    modes = {"kt": "force", "nt": False, None: table}
+    fns = {n: make_call(h, q, k, v, outs[n], causal, modes[mode]) for n, (h, mode) in libs.items()}
     names = list(libs)
     first = names[0]
 
@@ -148,7 +162,10 @@ def main():
     libs = {}
     for spec in args.libs:
         name, path = spec.split("=", 1)
-        libs[name] = load(path)
+        mode = None
+        if path.endswith("@kt") or path.endswith("@nt"):
+            path, mode = path[:-3], path[-2:]
+        libs[name] = (load(path), mode)
     results = {}
     for cfg in args.configs:
         print(f"ab: {cfg}, {len(libs)} builds, {args.rounds} rounds x {args.steps} steps", flush=True)
