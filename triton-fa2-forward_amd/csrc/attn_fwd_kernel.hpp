@@ -43,6 +43,12 @@
 #include "attn_fwd_common.hpp"
 #include "attn_fwd_schedule.hpp"
 
+// fp16 below head_dim 128 sums l from the unrounded P in fp32 (0) or from P rounded to fp16 with
+// v_dot2 (1); compile-time so that an A/B of two builds can compare them (ab.py).
+#ifndef FA2_FP16_ROUNDED_SUM
+#define FA2_FP16_ROUNDED_SUM 0
+#endif
+
 namespace fa2 {
 
 // The dynamic tail's program of tail workgroup `block` (tail_pick), with agent-scope atomic
@@ -334,7 +340,7 @@ void attn_fwd_kernel(const Params p) {
   // (+2.5% on C3's shape) and the fp32 one, as in the reference (fa2/kernel.py:98), at 64 and
   // below (C4: 9% faster; with it the fp16 pipelined loop needs 160 VGPRs, three waves per
   // SIMD, with the rounded sum 173, two).
-  constexpr bool kRoundedSum = DT == 1 || D == 128;
+  constexpr bool kRoundedSum = DT == 1 || D == 128 || FA2_FP16_ROUNDED_SUM;
   float m_i = -INFINITY;
   float l_i = 0.f;
   float l_exact = 0.f;

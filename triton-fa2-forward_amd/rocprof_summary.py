@@ -16,6 +16,8 @@ and this module writes, from those CSVs and the bench.py line in <root>/<cfg>_tr
   profiles/attn_fwd_kernel_<cfg>_sq_counters.md       instruction mix, MFMA busy, bank conflicts
   profiles/attn_fwd_kernel_utilisation_counters.md    per-unit busy fractions, all configs
   profiles/l2_miss_traffic.json                        the traffic figures bench.py reports
+and, from bench.py's JSON lines (--bench-log: `bench.py --all --sdpa --no-cpu-baseline` then
+`bench.py --pack-short --no-cpu-baseline`, appended to one log), profiles/bench_all_configs.md.
 
 L2-miss bytes: TCC FETCH_SIZE and WRITE_SIZE count, in KiB per dispatch, the requests that leave
 the L2; a plain device copy of known size read by the same counters gives the factor that turns
@@ -334,6 +336,64 @@ def write_util(root, cfgs, out_dir):
     return path, u
 
 
+def bench_lines(log_path):
+    """Every bench.py JSON line of a log, in order."""
+    out = []
+    with open(log_path) as f:
+        for ln in f:
+            if ln.startswith('{"metric"'):
+                out.append(json.loads(ln))
+    return out
+
+
+def write_bench(log_path, out_dir):
+    """profiles/bench_all_configs.md from bench.py's lines: the configs' TFLOP/s, clock and
+    roofline fractions, torch SDPA beside them, and the few-queries table."""
+    lines_ = bench_lines(log_path)
+    cfg = [b for b in lines_ if b.get("unit") == "TFLOP/s"]
+    short = [b for b in lines_ if b.get("unit") == "TB/s"]
+    env = cfg[0].get("env", {}) if cfg else {}
+    L = ["# bench.py on every configuration, one box, current build", "",
+         "Commands (from the repository root on the MI355X box):", "",
+         "    python bench.py --all --sdpa --no-cpu-baseline",
+         "    python bench.py --pack-short --no-cpu-baseline", "",
+         f"Box: {env.get('gpu', '?')} ({env.get('arch', '?')}), ROCm {env.get('rocm', '?')}, torch {env.get('torch', '?')}. "
+         "Each line is `bench.py`'s JSON line summarised: back-to-back steps after a 1 s clock "
+         "settle (`value`), the sampled graphics clock over the timed steps, `roofline.frac` "
+         "against the 2.4 GHz dense peak (2516.6 TFLOP/s) and at the sampled clock, the measured mix "
+         "ceiling with the kernel's VGPR accumulators, the reference's flushed per-launch protocol, "
+         "and torch's fused SDPA (AOTriton flash) on the same inputs, K/V expanded.", "",
+         "| config | TFLOP/s | ms per step | frac of peak | sclk MHz | frac at sampled sclk | frac of mix "
+         "ceiling (VGPR acc.) | reference protocol TFLOP/s | torch SDPA TFLOP/s |",
+         "|---|---|---|---|---|---|---|---|---|"]
+    for b in cfg:
+        r = b["roofline"]
+        sclk = b.get("clock", {}).get("timed_steps", {}).get("sclk_mhz_median")
+        sd = b.get("sdpa_same_box") or {}
+        ref = b.get("value_reference_protocol", {}).get("tflops")
+        L.append(f"| {b['config']['workload']} | {b['value']} | {b['ms_per_step']:.4f} | {r['frac']} | "
+                 f"{sclk if sclk else '-'} | {r.get('frac_at_sampled_sclk', '-')} | "
+                 f"{r.get('frac_of_measured_mix_ceiling_vgpr_acc', '-')} | {ref if ref else '-'} | "
+                 f"{sd.get('tflops', '-')} |")
+    if short:
+        L += ["", "Few queries against a long K/V (the reference's README.md:282-301 table; fp16, B 16, "
+                  "H 32/8, N_kv 4096, D 128, non-causal; K + V = 256 MiB read once per call):", "",
+              "| N_q | us per call | K/V read rate TB/s | frac of 8 TB/s | frac of a streaming read of the "
+              "same size | splits | reference H100 us | speedup |",
+              "|---|---|---|---|---|---|---|---|"]
+        for b in short:
+            r = b["roofline"]
+            L.append(f"| {b['config']['n_q']} | {b['us_per_step']} | {b['value']} | {r['frac']} | "
+                     f"{r.get('frac_of_measured_read_rate', '-')} | {b['config']['num_splits']} | "
+                     f"{b.get('reference_h100_us', '-')} | {b.get('vs_reference_h100', '-')}x |")
+    L += ["", "Made by `python triton-fa2-forward_amd/rocprof_summary.py --bench-log <log>` from the "
+              "runs' JSON lines.", ""]
+    path = os.path.join(out_dir, "bench_all_configs.md")
+    with open(path, "w") as f:
+        f.write("\n".join(L))
+    return path
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--root", default="gpurun_out/prof", help="profile_configs.sh's output folder")
@@ -343,7 +403,10 @@ def main():
     ap.add_argument("--label", default="current", help="kernel_build label in the JSON")
     ap.add_argument("--parts", nargs="+", default=["trace", "traffic", "sq", "util"],
                     choices=["trace", "traffic", "sq", "util"])
+    ap.add_argument("--bench-log", default=None, help="also write bench_all_configs.md from it")
     args = ap.parse_args()
+    if args.bench_log:
+        print(write_bench(args.bench_log, args.out))
     os.makedirs(args.out, exist_ok=True)
     for cfg in args.configs:
         if "trace" in args.parts:

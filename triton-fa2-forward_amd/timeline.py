@@ -31,6 +31,18 @@ sys.path.insert(0, HERE)
 sys.path.insert(0, os.path.dirname(HERE))
 
 WORDS = 6          # FA2_ABLATE_TIMELINE_WORDS
+MD_HEAD = """# Per-workgroup timeline: fa2::attn_fwd_kernel on {cfg} (one launch, MI355X)
+
+Commands (committed code only; the timeline instance is in libfa2_ablate.so):
+
+    python triton-fa2-forward_amd/timeline.py --config {cfg} --csv {csv}
+    python triton-fa2-forward_amd/timeline.py --config {cfg} --from-csv {csv} --md profiles/timeline_{cfg}.md
+
+Every workgroup of the timeline instance (the product kernel, bit for bit, plus s_memrealtime
+stamps at 100 MHz) records entry, prologue done (Q and the first K/V tiles in, first barrier),
+tile loop done and stores done, its K/V tile count and the hardware id of its CU. It waits for its
+stores before the last stamp, which the product kernel does not, so its span is a little longer.
+"""
 TICK_US = 0.01     # s_memrealtime runs at 100 MHz
 
 
@@ -171,12 +183,22 @@ def main():
     ap.add_argument("--launches", type=int, default=20, help="launches before the recorded one")
     ap.add_argument("--csv", default=None, help="also write the per-workgroup rows here")
     ap.add_argument("--from-csv", default=None, help="summarise rows a previous --csv wrote (no GPU)")
+    ap.add_argument("--md", default=None,
+                    help="with --from-csv: write the summary as a profile (profiles/timeline_<cfg>.md)")
     args = ap.parse_args()
     if args.from_csv:
         import bench
 
         dt, causal, B, hq, hkv, n, d, scale, outl = bench.WORKLOADS[args.config]
-        print(summarize_rows(rows_from_csv(args.from_csv), bench.attn_flops(B, hq, n, n, d, causal))[1])
+        text = summarize_rows(rows_from_csv(args.from_csv), bench.attn_flops(B, hq, n, n, d, causal))[1]
+        if args.md:
+            with open(args.from_csv + ".head") if os.path.exists(args.from_csv + ".head") else \
+                    open(os.devnull) as f:
+                head = f.read().strip()
+            with open(args.md, "w") as f:
+                f.write(MD_HEAD.format(cfg=args.config, csv=args.from_csv) + "\n" + head + "\n\n"
+                        + text + "\n")
+        print(text)
         return
 
     import torch
@@ -203,10 +225,13 @@ def main():
     prod_ms, _ = bench.time_steps(lambda: _lib.attn_fwd(q, k, v, o, causal, 1, 128, 0, scale, stream),
                                   steps, 5)
     rows, text = summarize(recs, flops)
-    print(f"{bench.describe(args.config)}; output bit-exact with the product kernel; product kernel "
-          f"back to back {prod_ms / steps * 1e3:.2f} us per launch")
+    head = (f"{bench.describe(args.config)}; output bit-exact with the product kernel; product kernel "
+            f"back to back {prod_ms / steps * 1e3:.2f} us per launch")
+    print(head)
     print(text)
     if args.csv:
+        with open(args.csv + ".head", "w") as f:
+            f.write(head + "\n")
         with open(args.csv, "w") as f:
             f.write("block,start_us,prologue_us,loop_us,epilogue_us,end_us,tiles,xcc,se,sh,cu\n")
             for r in rows:
