@@ -14,8 +14,8 @@
  * memory (a static array, loaded as zeros; no allocation), which every launch leaves at zero
  * again. Each (device, stream) has its own set of words, so calls on different streams and
  * threads may overlap freely; a launch that uses a set first makes its stream wait for an event
- * the set's previous launch recorded, so a stream created with the handle of a destroyed one
- * never meets the old stream's launches on the words. Launches recorded under stream capture,
+ * that the set's previous launch signalled when it ended (its stop event), so a stream created
+ * with the handle of a destroyed one never meets the old stream's launches on the words. Launches recorded under stream capture,
  * launches on the per-thread default stream or on a stream of another device than the current
  * one, and launches past 256 streams per device run the static order instead. Either way the
  * output is the same, bit for bit. The order of programs follows the device's CU and XCD counts,

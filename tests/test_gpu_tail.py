@@ -21,7 +21,7 @@ workgroup runs a program changes from launch to launch; what the program compute
   the tail, bit for bit;
 * a stream destroyed with launches still queued and a new stream created at once (the handle can
   come back while the old launches run): every ticket set's launch waits for the event its previous
-  launch recorded, so the old and new launches never share the words at once.
+  launch signalled when it ended, so the old and new launches never share the words at once.
 
 The CPU tier (tests/test_schedule.py) checks the same ticket rules over thousands of shapes.
 """
@@ -169,7 +169,7 @@ def test_capture_records_the_static_order():
 def test_a_new_stream_on_a_reused_handle_keeps_the_tail_exact():
     """A stream is destroyed with tail launches still queued on it (hipStreamDestroy need not
     wait for them) and a new stream is created at once, which can get the same handle and so the
-    same ticket set; its launches wait for the event the old stream's last launch recorded, so
+    same ticket set; its launches wait for the event the old stream's last launch signalled, so
     the two never use the set's words at once. Streams created and destroyed through the HIP
     runtime directly (torch pools its own)."""
     import ctypes

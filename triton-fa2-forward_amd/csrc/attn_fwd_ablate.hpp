@@ -37,11 +37,11 @@ constexpr bool ablation_variant_built(int variant) {
 // 128 rows; variant must be one of kAblationVariants. Returns a hipError_t value.
 template <int DT, int D>
 int launch_attn_fwd_ablate(const Params& p, int variant, bool causal, unsigned grid,
-                           hipStream_t stream);
+                           hipStream_t stream, hipEvent_t stop);
 
 #define FA2_DECLARE_ABLATE(DT, D)                                                          \
   extern template int launch_attn_fwd_ablate<DT, D>(const Params&, int, bool, unsigned, \
-                                                    hipStream_t);
+                                                    hipStream_t, hipEvent_t);
 FA2_DECLARE_ABLATE(0, 16)
 FA2_DECLARE_ABLATE(0, 32)
 FA2_DECLARE_ABLATE(0, 64)

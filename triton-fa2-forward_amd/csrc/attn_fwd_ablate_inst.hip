@@ -13,7 +13,7 @@ namespace fa2 {
 namespace {
 
 template <int DT, int D, int VARIANT>
-int launch_variant(const Params& p, bool causal, unsigned grid, hipStream_t s) {
+int launch_variant(const Params& p, bool causal, unsigned grid, hipStream_t s, hipEvent_t stop) {
   constexpr int BN = default_block_n(D);
   if constexpr ((VARIANT & kVariantSplitKeys) != 0) {
     // the key split: 8 waves, two groups of 4 on the same 128 rows; head_dim 128 only
@@ -21,28 +21,24 @@ int launch_variant(const Params& p, bool causal, unsigned grid, hipStream_t s) {
       return (int)hipErrorInvalidValue;
     } else {
       if (causal)
-        hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 8, BN, true, VARIANT>), dim3(grid), dim3(512),
-                           0, s, p);
-      else
-        hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 8, BN, false, VARIANT>), dim3(grid), dim3(512),
-                           0, s, p);
-      return (int)hipGetLastError();
+        return launch_with_stop(attn_fwd_kernel<DT, D, 8, BN, true, VARIANT>, grid, 512, s, stop,
+                                p);
+      return launch_with_stop(attn_fwd_kernel<DT, D, 8, BN, false, VARIANT>, grid, 512, s, stop,
+                              p);
     }
   } else {
     if (causal)
-      hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, true, VARIANT>), dim3(grid), dim3(256), 0,
-                         s, p);
-    else
-      hipLaunchKernelGGL((attn_fwd_kernel<DT, D, 4, BN, false, VARIANT>), dim3(grid), dim3(256),
-                         0, s, p);
-    return (int)hipGetLastError();
+      return launch_with_stop(attn_fwd_kernel<DT, D, 4, BN, true, VARIANT>, grid, 256, s, stop, p);
+    return launch_with_stop(attn_fwd_kernel<DT, D, 4, BN, false, VARIANT>, grid, 256, s, stop, p);
   }
 }
 
 template <int DT, int D, int... V>
-int dispatch(const Params& p, int variant, bool causal, unsigned grid, hipStream_t s) {
+int dispatch(const Params& p, int variant, bool causal, unsigned grid, hipStream_t s,
+             hipEvent_t stop) {
   int rc = (int)hipErrorInvalidValue;
-  (void)((variant == V ? (rc = launch_variant<DT, D, V>(p, causal, grid, s), true) : false) || ...);
+  (void)((variant == V ? (rc = launch_variant<DT, D, V>(p, causal, grid, s, stop), true) : false) ||
+         ...);
   return rc;
 }
 
@@ -50,17 +46,17 @@ int dispatch(const Params& p, int variant, bool causal, unsigned grid, hipStream
 
 template <int DT, int D>
 int launch_attn_fwd_ablate(const Params& p, int variant, bool causal, unsigned grid,
-                           hipStream_t s) {
+                           hipStream_t s, hipEvent_t stop) {
   return dispatch<DT, D, kAblationVariants[0], kAblationVariants[1], kAblationVariants[2],
                   kAblationVariants[3], kAblationVariants[4], kAblationVariants[5],
                   kAblationVariants[6], kAblationVariants[7], kAblationVariants[8],
                   kAblationVariants[9], kAblationVariants[10]>(
-      p, variant, causal, grid, s);
+      p, variant, causal, grid, s, stop);
 }
 
 static_assert(sizeof(kAblationVariants) / sizeof(int) == 11, "dispatch lists every variant");
 
 template int launch_attn_fwd_ablate<FA2_DT, FA2_D>(const Params&, int, bool, unsigned,
-                                                   hipStream_t);
+                                                   hipStream_t, hipEvent_t);
 
 }  // namespace fa2

@@ -144,6 +144,12 @@ int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim, const Topology
 //   FA2_TAIL_SHARE_PCT    the tail's share of each XCD's programs (at most)
 //   FA2_TAIL_CHUNK_PCT    ... and of one unit chunk's programs (at most)
 //   FA2_TAIL_EXTRA_PCT    spare tail workgroups, in percent of the grid
+//   FA2_TAIL_EVENT_GUARD  1: each ticket set's launch waits for the event its previous launch
+//                         signalled on completion (below); 0: no events, for measuring what
+//                         they cost only (unsafe with streams destroyed while their work runs)
+#ifndef FA2_TAIL_EVENT_GUARD
+#define FA2_TAIL_EVENT_GUARD 1
+#endif
 #ifndef FA2_TAIL_PRIVATE_PCT
 #define FA2_TAIL_PRIVATE_PCT 0
 #endif
@@ -229,10 +235,11 @@ TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, in
 // different streams overlap freely, and launches on one stream run one after another. A stream's
 // handle can be reused by a stream created after it is destroyed, while the old stream's work
 // may still be running (hipStreamDestroy does not promise to wait for it). So every set also has
-// an event, recorded on the launch's stream after each launch that used the set, and the next
-// launch that uses the set first makes its stream wait for that event: a new stream under an old
-// handle then starts its launch only once the old one has ended. On one stream the wait costs
-// nothing. Past kTicketSets streams per device, launches run the static order.
+// an event, which each launch that uses the set signals when it ends (the kernel is launched with
+// it as its stop event), and the next launch that uses the set first makes its stream wait for
+// that event: a new stream under an old handle then starts its launch only once the old one has
+// ended. On one stream the wait costs nothing. Past kTicketSets streams per device, launches run
+// the static order.
 constexpr int kTicketSets = 256;
 constexpr int kTicketDevices = 64;
 
@@ -243,7 +250,7 @@ namespace {
 
 struct TicketSet {
   int index = -1;
-  hipEvent_t last = nullptr;  // recorded after the last launch that used the set
+  hipEvent_t last = nullptr;  // signalled when the last launch that used the set ended
   bool recorded = false;
 };
 
@@ -350,7 +357,8 @@ TicketSet* acquire_tickets(hipStream_t stream, int dev, uint32_t** words) {
     set->last = ev;
   }
   if (set->index < 0) return nullptr;  // retired (an event record failed)
-  if (set->recorded && hipStreamWaitEvent(stream, set->last, 0) != hipSuccess) {
+  if (FA2_TAIL_EVENT_GUARD && set->recorded &&
+      hipStreamWaitEvent(stream, set->last, 0) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
@@ -358,23 +366,24 @@ TicketSet* acquire_tickets(hipStream_t stream, int dev, uint32_t** words) {
   return set;
 }
 
-// After the launch that used `set`: record its event on the stream. If that fails, the set is
-// retired (never handed out again), since a later launch could no longer wait for this one.
-void finish_tickets(TicketSet* set, hipStream_t stream) {
+// After the launch that used `set`, which signals the set's event when it ends: the next launch
+// on the set waits for it. If the launch failed, the event's state is unknown and the set is
+// retired (never handed out again).
+void finish_tickets(TicketSet* set, bool launched) {
+  if (!FA2_TAIL_EVENT_GUARD) return;
   DeviceTable& t = device_table();
   std::lock_guard<std::mutex> lock(t.mu);
-  if (hipEventRecord(set->last, stream) == hipSuccess) {
+  if (launched)
     set->recorded = true;
-  } else {
-    (void)hipGetLastError();
+  else
     set->index = -1;
-  }
 }
 
 // Launches the attention kernel of one checked call: the product's instances in the library,
 // the timing variants (variant != 0) in the measurement library. Returns a hipError_t value.
 using KernelLaunch = int (*)(int dtype, int di, const Params& p, int waves, int block_n,
-                             bool causal, unsigned grid, hipStream_t s, int variant);
+                             bool causal, unsigned grid, hipStream_t s, int variant,
+                             hipEvent_t stop);
 
 // One call's arguments, as the C ABI takes them.
 struct LaunchArgs {
@@ -640,10 +649,14 @@ int attn_fwd_impl(const LaunchArgs& a, KernelLaunch launch_kernel, void* stream)
       grid -= pl.tail.tail_wgs - pl.tail.programs();  // the static order: one workgroup a program
     }
   }
+  // the ticket set's event, signalled by the kernel's own completion (hipExtLaunchKernel): a
+  // marker of its own behind each launch (hipEventRecord) cost 0.6-1.8% (C3, C2, fp16 head_dim
+  // 64), the event on the launch nothing measurable (same-box A/B)
+  hipEvent_t stop = (set && FA2_TAIL_EVENT_GUARD) ? set->last : nullptr;
   int e = launch_kernel(a.dtype, pl.di, p, pl.waves, pl.bn, a.causal != 0, (unsigned)grid, st,
-                        a.variant);
+                        a.variant, stop);
   if (set) {
-    finish_tickets(set, st);
+    finish_tickets(set, e == hipSuccess);
     if (e == hipSuccess) g_tail_launches.fetch_add(1, std::memory_order_relaxed);
   }
   if (e != hipSuccess)

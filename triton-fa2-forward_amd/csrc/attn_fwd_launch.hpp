@@ -4,17 +4,32 @@
 // dtype x head_dim), so the library's many kernel instances build in parallel.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "attn_fwd_params.hpp"
 
 namespace fa2 {
 
+// One kernel launch on `stream`; with a `stop` event, through hipExtLaunchKernel, which signals
+// the event from the kernel's own completion instead of a marker of its own in the stream.
+// Returns a hipError_t value.
+template <class Kernel>
+int launch_with_stop(Kernel kernel, unsigned grid, unsigned block, hipStream_t stream,
+                     hipEvent_t stop, const Params& p) {
+  if (stop)
+    hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, nullptr, stop, 0, p);
+  else
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
 // Launches attn_fwd_kernel<DT, D, waves, block_n, causal> on `grid` programs.
-// waves in {1, 2, 4, 8}, block_n in {32, 64, 128}. Returns a hipError_t value.
+// waves in {1, 2, 4, 8}, block_n in {32, 64, 128}; `stop` (or null) is signalled when the kernel
+// ends. Returns a hipError_t value.
 template <int DT, int D>
 int launch_attn_fwd(const Params& p, int waves, int block_n, bool causal, unsigned grid,
-                    hipStream_t stream);
+                    hipStream_t stream, hipEvent_t stop);
 
 // gfx950 default K/V tile: 64 keys (sweep.py on the BASELINE.json configs, MI355X: best for
 // C2, C3, C5 at head_dim 128, and for C4 at head_dim 64 with the software-pipelined loop that
@@ -37,7 +52,7 @@ hipError_t noalloc_scratch(int dev, void** out);
 
 #define FA2_DECLARE_LAUNCH(DT, D)                                                          \
   extern template int launch_attn_fwd<DT, D>(const Params&, int, int, bool, unsigned, \
-                                             hipStream_t);
+                                             hipStream_t, hipEvent_t);
 FA2_DECLARE_LAUNCH(0, 16)
 FA2_DECLARE_LAUNCH(0, 32)
 FA2_DECLARE_LAUNCH(0, 64)

@@ -13,18 +13,18 @@
 namespace {
 
 int launch_ablate(int dtype, int di, const Params& p, int waves, int block_n, bool causal,
-                  unsigned grid, hipStream_t s, int variant) {
+                  unsigned grid, hipStream_t s, int variant, hipEvent_t stop) {
   // the variants exist at the default configuration only (4 waves of 32 rows, the default tile)
   if (waves != 4 || block_n != default_block_n(kDims[di])) return (int)hipErrorInvalidValue;
   switch (dtype * 4 + di) {
-    case 0: return fa2::launch_attn_fwd_ablate<0, 16>(p, variant, causal, grid, s);
-    case 1: return fa2::launch_attn_fwd_ablate<0, 32>(p, variant, causal, grid, s);
-    case 2: return fa2::launch_attn_fwd_ablate<0, 64>(p, variant, causal, grid, s);
-    case 3: return fa2::launch_attn_fwd_ablate<0, 128>(p, variant, causal, grid, s);
-    case 4: return fa2::launch_attn_fwd_ablate<1, 16>(p, variant, causal, grid, s);
-    case 5: return fa2::launch_attn_fwd_ablate<1, 32>(p, variant, causal, grid, s);
-    case 6: return fa2::launch_attn_fwd_ablate<1, 64>(p, variant, causal, grid, s);
-    default: return fa2::launch_attn_fwd_ablate<1, 128>(p, variant, causal, grid, s);
+    case 0: return fa2::launch_attn_fwd_ablate<0, 16>(p, variant, causal, grid, s, stop);
+    case 1: return fa2::launch_attn_fwd_ablate<0, 32>(p, variant, causal, grid, s, stop);
+    case 2: return fa2::launch_attn_fwd_ablate<0, 64>(p, variant, causal, grid, s, stop);
+    case 3: return fa2::launch_attn_fwd_ablate<0, 128>(p, variant, causal, grid, s, stop);
+    case 4: return fa2::launch_attn_fwd_ablate<1, 16>(p, variant, causal, grid, s, stop);
+    case 5: return fa2::launch_attn_fwd_ablate<1, 32>(p, variant, causal, grid, s, stop);
+    case 6: return fa2::launch_attn_fwd_ablate<1, 64>(p, variant, causal, grid, s, stop);
+    default: return fa2::launch_attn_fwd_ablate<1, 128>(p, variant, causal, grid, s, stop);
   }
 }
 

@@ -14,17 +14,17 @@ namespace {
 // The product's kernel instances, per (dtype, head_dim) each compiled in its own translation
 // unit. This library has no timing variants (the measurement library fa2_ablate.hip has them).
 int launch(int dtype, int di, const Params& p, int waves, int block_n, bool causal, unsigned grid,
-           hipStream_t s, int variant) {
+           hipStream_t s, int variant, hipEvent_t stop) {
   if (variant != 0) return (int)hipErrorInvalidValue;
   switch (dtype * 4 + di) {
-    case 0: return fa2::launch_attn_fwd<0, 16>(p, waves, block_n, causal, grid, s);
-    case 1: return fa2::launch_attn_fwd<0, 32>(p, waves, block_n, causal, grid, s);
-    case 2: return fa2::launch_attn_fwd<0, 64>(p, waves, block_n, causal, grid, s);
-    case 3: return fa2::launch_attn_fwd<0, 128>(p, waves, block_n, causal, grid, s);
-    case 4: return fa2::launch_attn_fwd<1, 16>(p, waves, block_n, causal, grid, s);
-    case 5: return fa2::launch_attn_fwd<1, 32>(p, waves, block_n, causal, grid, s);
-    case 6: return fa2::launch_attn_fwd<1, 64>(p, waves, block_n, causal, grid, s);
-    default: return fa2::launch_attn_fwd<1, 128>(p, waves, block_n, causal, grid, s);
+    case 0: return fa2::launch_attn_fwd<0, 16>(p, waves, block_n, causal, grid, s, stop);
+    case 1: return fa2::launch_attn_fwd<0, 32>(p, waves, block_n, causal, grid, s, stop);
+    case 2: return fa2::launch_attn_fwd<0, 64>(p, waves, block_n, causal, grid, s, stop);
+    case 3: return fa2::launch_attn_fwd<0, 128>(p, waves, block_n, causal, grid, s, stop);
+    case 4: return fa2::launch_attn_fwd<1, 16>(p, waves, block_n, causal, grid, s, stop);
+    case 5: return fa2::launch_attn_fwd<1, 32>(p, waves, block_n, causal, grid, s, stop);
+    case 6: return fa2::launch_attn_fwd<1, 64>(p, waves, block_n, causal, grid, s, stop);
+    default: return fa2::launch_attn_fwd<1, 128>(p, waves, block_n, causal, grid, s, stop);
   }
 }
 
