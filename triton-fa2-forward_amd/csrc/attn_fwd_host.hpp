@@ -178,10 +178,14 @@ int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim, const Topology
 // program the same work, so no light programs to even out the end) lost 0.3% and keep the static
 // order; so do grids of fewer than two rounds per XCD.
 // One shared counter hands a program to whichever XCD asks, so its unit's K/V is fetched into a
-// second L2 (C3's reads past L2 rose from 213.6 to 334.1 MB per launch). So the XCD-aware order
-// gives each XCD a queue of its own: the heavier FA2_TAIL_PRIVATE_PCT% of its tail programs stay
-// with its workgroups, and only the lightest go to the shared pool. Grids in the fallback order
-// have no XCD affinity to keep and use the shared pool alone.
+// second L2 (C3's reads past L2 rose from 213.6 to 334.1 MB per launch). A build with
+// FA2_TAIL_PRIVATE_PCT > 0 gives each XCD of the XCD-aware order a queue of its own: the heavier
+// FA2_TAIL_PRIVATE_PCT% of its tail programs stay with its workgroups, and only the lightest go to
+// the shared pool. That brings the L2 locality back (C3 337 -> 214 MB per launch at 100%) but
+// costs time (C3 -2.2%, fp16 head_dim 64 causal -2.0%, same-box A/B at 50%): only programs that
+// any XCD can take even out the XCDs' clocks, and the extra L2 misses cost nothing measurable
+// (C3 moves ~0.7 TB/s past L2). So the default is 0: one shared pool. Grids in the fallback
+// order have no XCD affinity to keep and use the shared pool alone.
 struct TailSchedule {
   int32_t static_blocks = 0, tail_wgs = 0;  // tail_wgs == 0: static order
   int32_t queues = 1, private_per_queue = 0, shared = 0;
