@@ -4,11 +4,12 @@ attn_fwd_schedule.hpp: tail_pick).
 Where a causal grid has at least two rounds of programs per XCD, the last programs of every XCD's
 static order (program_of's XCD order, or its fallback order where the (batch, kv head) units do
 not split evenly over the 8 XCDs) are dealt at run time: each workgroup past the static part
-takes a ticket from its XCD's queue word (that XCD's own heavier tail programs) and, once its
-queue has none left for it, from the launch's shared word (the lightest tail programs, for
-whichever XCD asks). Every word is incremented a fixed number of times per launch and wraps, so it
-is zero again after every launch, and a few spare workgroups find no program and exit. Which
-workgroup runs a program changes from launch to launch; what the program computes does not. So:
+takes a ticket from the launch's shared word, which deals the tail programs to whichever XCD
+asks (a build with FA2_TAIL_PRIVATE_PCT > 0 first gives each XCD a queue word of its own for its
+heavier tail programs; tests/test_schedule.py checks those rules on the CPU). Every word is
+incremented a fixed number of times per launch and wraps, so it is zero again after every launch,
+and a few spare workgroups find no program and exit. Which workgroup runs a program changes from
+launch to launch; what the program computes does not. So:
 
 * the output equals the static order's (the measurement library's FA2_ABLATE_STATIC_ORDER) bit
   for bit, on shapes with and without GQA packing, ragged, at head_dim 64 and 128;
@@ -21,7 +22,8 @@ workgroup runs a program changes from launch to launch; what the program compute
   the tail, bit for bit;
 * a stream destroyed with launches still queued and a new stream created at once (the handle can
   come back while the old launches run): every ticket set's launch waits for the event its previous
-  launch signalled when it ended, so the old and new launches never share the words at once.
+  launch signalled when it ended, so the old and new launches never share the words at once;
+* streams past the 256 ticket sets a device has run the static order, with the same bits.
 
 The CPU tier (tests/test_schedule.py) checks the same ticket rules over thousands of shapes.
 """
@@ -199,6 +201,59 @@ def test_a_new_stream_on_a_reused_handle_keeps_the_tail_exact():
     print(f"stream handles: {len(set(handles))} distinct of {len(handles)}", flush=True)
     for out in outs:
         assert torch.equal(out, want)
+
+
+def test_streams_past_the_ticket_sets_run_the_static_order():
+    """300 streams that stay alive, one launch of the measurement library on each: the library's
+    count of tail launches grows by one for each new stream until its 256 ticket sets are handed
+    out (some may have gone to streams of earlier tests in this process) and then stays put; every
+    launch, with a tail or without, gives the static order's bits."""
+    import ctypes
+    import math
+
+    from ablation import ablate_lib
+    from fa2 import _lib
+    from fa2.kernel import LOG2E
+
+    lib = ablate_lib()
+    lib.fa2_ablate_tail_launches.restype = ctypes.c_longlong
+    lib.fa2_ablate_tail_launches.argtypes = []
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    q, k, v, _ = _inputs("gqa_d128", seed=13)
+    want = _static(q, k, v, False)
+    out = torch.empty_like(q)
+    torch.cuda.synchronize()
+    B, H_q, N, D = q.shape
+    strides = [_lib._strides(t) for t in (q, k, v, out)]
+    took, handles = [], []
+    try:
+        for i in range(300):
+            h = ctypes.c_void_p()
+            assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+            handles.append(h.value)
+            before = lib.fa2_ablate_tail_launches()
+            out.zero_()
+            torch.cuda.synchronize()
+            rc = lib.fa2_ablate_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                         *strides, B, H_q, k.shape[1], N, N, D,
+                                         _lib.DTYPE_CODE[q.dtype], 1, 1, LOG2E / math.sqrt(D), 0,
+                                         h.value)
+            assert rc == 0, lib.fa2_ablate_last_error().decode()
+            assert hip.hipStreamSynchronize(h) == 0
+            took.append(lib.fa2_ablate_tail_launches() - before)
+            assert torch.equal(out, want), f"stream {i} (tail: {took[-1]})"
+    finally:
+        for h in handles:
+            hip.hipStreamSynchronize(h)
+            hip.hipStreamDestroy(h)
+    first_static = took.index(0) if 0 in took else len(took)
+    print(f"streams with a ticket set: {first_static} of {len(took)}", flush=True)
+    assert set(took) <= {0, 1}
+    assert took == [1] * first_static + [0] * (len(took) - first_static)
+    assert 1 <= first_static <= 256
 
 
 @pytest.mark.parametrize("block_n", [32, 64, 128])
