@@ -12,10 +12,12 @@
  * Causal grids of at least two rounds of programs per XCD deal their last programs at run time
  * (a dynamic tail): their workgroups take tickets from counter words in the library's own device
  * memory (a static array, loaded as zeros; no allocation), which every launch leaves at zero
- * again. Each (device, stream) has its own set of words, so calls on different streams and
- * threads may overlap freely; a launch that uses a set first makes its stream wait for an event
- * that the set's previous launch signalled when it ended (its stop event), so a stream created
- * with the handle of a destroyed one never meets the old stream's launches on the words. Launches recorded under stream capture,
+ * again. Each (device, stream) has its own set of words, made at the stream's first such launch
+ * together with one event (hipEventCreateWithFlags; the only object the library creates for a
+ * stream), so calls on different streams and threads may overlap freely; a launch that uses a set
+ * first makes its stream wait for the event, which the set's previous launch signalled when it
+ * ended (its stop event), so a stream created with the handle of a destroyed one never meets the
+ * old stream's launches on the words. Launches recorded under stream capture,
  * launches on the per-thread default stream or on a stream of another device than the current
  * one, and launches past 256 streams per device run the static order instead. Either way the
  * output is the same, bit for bit. The order of programs follows the device's CU and XCD counts,
@@ -123,7 +125,10 @@ FA2_API int fa2_attn_fwd_ex(const void* q, const void* k, const void* v, void* o
 /*
  * fa2_attn_fwd_noalloc - fa2_attn_fwd_ex without the workspace arguments: it allocates nothing.
  * No counterpart in the reference. It is for callers that cannot allocate device memory: code
- * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. It creates no
+ * event either: it deals a causal grid's tail only on a stream that already has a ticket set
+ * (from an earlier fa2_attn_fwd or fa2_attn_fwd_ex call on it) and runs the static order
+ * elsewhere, with the same output bit for bit.
  *
  * The split-KV partials and, where it pays, the key-norm table live in a device array owned by
  * the library, FA2_NOALLOC_SCRATCH_BYTES per GPU. The array sits in a device code object of its

@@ -149,3 +149,43 @@ def test_noalloc_under_graph_capture_replays_exactly(case):
         assert torch.equal(out, ref_out), seed
         if want_lse:
             assert torch.equal(lse, ref_lse), seed
+
+
+def test_noalloc_on_new_and_known_streams_equals_workspace_launch():
+    """A causal grid with a dynamic tail through fa2_attn_fwd_noalloc on a stream the library has
+    not seen (no ticket set: the no-allocation entry point makes none, since a set's event is a
+    runtime object, and runs the static order) and on the same stream after a fa2_attn_fwd_ex call
+    there gave it a set (the tail): both equal fa2_attn_fwd_ex's output bit for bit. The stream
+    is made through the HIP runtime directly (torch pools its own)."""
+    import ctypes
+
+    from fa2 import _lib
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    q, k, v = make_qkv(1, 32, 8, 4096, 4096, 128, torch.bfloat16, seed=21)
+    print("noalloc on a new stream: B=1 Hq=32 Hkv=8 N=4096 D=128 bf16 causal", flush=True)
+    want, _, _ = _run_ex(q, k, v, True, 1, False)
+    torch.cuda.synchronize()
+    h = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+    try:
+        outs = []
+        for step in ("new", "ex", "known"):
+            out = torch.empty_like(q)
+            if step == "ex":
+                nbytes = _lib.workspace_bytes_for(1, 32, 8, 4096, 4096, 128, q.dtype, True, 1)
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+                _lib.attn_fwd_ex(q, k, v, out, True, 1, 128, 0, _scale(128), None, 1,
+                                 ws if nbytes else None, h.value)
+            else:
+                _lib.attn_fwd_noalloc(q, k, v, out, True, 1, 128, 0, _scale(128), None, 1, h.value)
+            assert hip.hipStreamSynchronize(h) == 0
+            outs.append((step, out))
+        for step, out in outs:
+            assert torch.equal(out, want), step
+    finally:
+        hip.hipStreamSynchronize(h)
+        hip.hipStreamDestroy(h)

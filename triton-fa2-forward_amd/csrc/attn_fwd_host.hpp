@@ -319,9 +319,11 @@ Topology device_topology(int dev) {
 // being recorded under stream capture (a graph can be instantiated twice and both instances run
 // at once, which would share the set), one on the per-thread default stream (its handle names
 // another stream in every thread), one on a stream of another device than the current one, or
-// when no set or event is to be had. Runtime errors met here are cleared, so that the launch
-// after it does not report them. finish_tickets() must follow the launch.
-TicketSet* acquire_tickets(hipStream_t stream, int dev, uint32_t** words) {
+// when no set or event is to be had. With may_create false, only a stream that already has a set
+// gets it (making a set creates an event, which a caller that allocates nothing must not do).
+// Runtime errors met here are cleared, so that the launch after it does not report them.
+// finish_tickets() must follow the launch.
+TicketSet* acquire_tickets(hipStream_t stream, int dev, uint32_t** words, bool may_create) {
   *words = nullptr;
   if (stream == hipStreamPerThread || dev < 0 || dev >= kTicketDevices) return nullptr;
   int cur = -1;
@@ -337,6 +339,8 @@ TicketSet* acquire_tickets(hipStream_t stream, int dev, uint32_t** words) {
   DeviceTable& t = device_table();
   std::lock_guard<std::mutex> lock(t.mu);
   DeviceState& d = t.dev[dev];
+  const auto it = d.by_stream.find(stream);
+  if (it == d.by_stream.end() && !may_create) return nullptr;
   if (!d.ticket_base) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_ticket_words)) != hipSuccess || !p) {
@@ -346,7 +350,6 @@ TicketSet* acquire_tickets(hipStream_t stream, int dev, uint32_t** words) {
     d.ticket_base = static_cast<uint32_t*>(p);
   }
   TicketSet* set;
-  const auto it = d.by_stream.find(stream);
   if (it != d.by_stream.end()) {
     set = &it->second;
   } else {
@@ -404,6 +407,8 @@ struct LaunchArgs {
   uint64_t* timeline;
   int64_t timeline_words;
   bool static_order;
+  // false: the launch may use its stream's ticket set but not make one (fa2_attn_fwd_noalloc)
+  bool new_ticket_set = true;
 };
 
 // A checked call, ready to launch: the kernel's arguments (without the key-norm table and the
@@ -646,7 +651,7 @@ int attn_fwd_impl(const LaunchArgs& a, KernelLaunch launch_kernel, void* stream)
   int64_t grid = pl.grid;
   if (pl.tail.tail_wgs > 0) {
     uint32_t* words = nullptr;
-    set = acquire_tickets(st, dev, &words);
+    set = acquire_tickets(st, dev, &words, a.new_ticket_set);
     if (set) {
       apply_tail(pl, words);
     } else {

@@ -175,7 +175,7 @@ int fa2_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
   }
   const LaunchArgs a{q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
                      n_q, n_kv, head_dim, dtype, causal, pack, block_m, block_n, qk_scale, lse,
-                     num_splits, ws, use, 0, nullptr, 0, false};
+                     num_splits, ws, use, 0, nullptr, 0, false, false};
   return attn_fwd_impl(a, launch, stream);
 }
 
