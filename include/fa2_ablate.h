@@ -45,6 +45,12 @@ extern "C" {
  * What halving the longest program's key range buys against losing the second workgroup per
  * CU. */
 #define FA2_ABLATE_SPLIT_KEYS 512
+/* Not in the reference: a program's fixed cost knocked out (outputs wrong on purpose). NO_Q_LOAD:
+ * Q is not read (a lane pattern of small values in its registers); NO_STORE: nothing is written
+ * (the results are only kept alive). What hiding a program's Q load or its output store behind
+ * another program's tiles could gain at most. */
+#define FA2_ABLATE_NO_Q_LOAD 1024
+#define FA2_ABLATE_NO_STORE 2048
 /* Not a kernel switch and not in the reference: the launch keeps the static order of programs
  * (workgroup b runs program b) where fa2_attn_fwd deals a causal grid's last programs at run
  * time (its dynamic tail). Combines with any variant; the output is the same bit for bit. */

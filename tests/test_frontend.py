@@ -411,10 +411,10 @@ def test_measurement_library_exports_exactly_its_header():
         "fa2_ablate_hbm_read", "fa2_ablate_tail_schedule", "fa2_ablate_program_map",
         "fa2_ablate_tail_launches", "fa2_ablate_last_error"}
     # the knockouts are compiled into it: kernel instances with the no_exp, no_softmax and
-    # kv_l2 bits, matmul_only (no_softmax | kv_l2), no_kv_staging (256) and the key split (512,
-    # head_dim 128 only); and the timeline instance (64)
+    # kv_l2 bits, matmul_only (no_softmax | kv_l2), no_kv_staging (256), the key split (512,
+    # head_dim 128 only), no_q_load (1024) and no_store (2048); and the timeline instance (64)
     variants = {int(m.group(1)) for n in names for m in [re.search(r"ELb[01]ELi(\d+)EEEv", n)] if m}
-    assert variants == {0, 1, 2, 3, 8, 16, 32, 48, 64, 256, 512}
+    assert variants == {0, 1, 2, 3, 8, 16, 32, 48, 64, 256, 512, 1024, 2048}
 
 
 @needs_ablate
@@ -493,9 +493,11 @@ def test_ablation_front_end_checks_arguments_on_the_cpu():
     # the reference's variant names (bench/ablation.py:42-53) and their bits
     assert list(VARIANTS) == ["copy", "scale_first", "mask_every_tile", "before_fixes", "no_exp",
                               "no_softmax", "kv_l2", "matmul_only", "no_kv_staging", "split_keys",
-                              "pack", "static_order"]
+                              "no_q_load", "no_store", "pack", "static_order"]
     assert variant_bits(VARIANTS["matmul_only"]) == 48
     assert variant_bits(VARIANTS["no_kv_staging"]) == 256  # FA2_ABLATE_NO_KV_STAGING
+    assert variant_bits(VARIANTS["no_q_load"]) == 1024  # FA2_ABLATE_NO_Q_LOAD
+    assert variant_bits(VARIANTS["no_store"]) == 2048  # FA2_ABLATE_NO_STORE
     assert variant_bits(VARIANTS["static_order"]) == 128  # FA2_ABLATE_STATIC_ORDER, host-only
     q = torch.zeros(1, 4, 8, 64, dtype=torch.float16)
     with pytest.raises(AssertionError, match="unknown"):

@@ -10,10 +10,13 @@ reference tests its knockout copy (tests/test_ablation.py:16-48):
 * the key split (8 waves in two groups over the halves of each program's key range, merged
   through LDS) is still attention: the 2x-SDPA rule against the fp64 oracle on ragged, GQA,
   causal and full shapes, and C5 at full size against the fp32 oracle;
-* the work-skipping knockouts (no_exp, no_softmax, kv_l2, matmul_only, no_kv_staging) change the output
-  (tests/test_ablation.py:28-34), on both of the kernel's tile loops (software-pipelined at
-  head_dim 64, one tile at a time otherwise), causal or not.
+* the work-skipping knockouts (no_exp, no_softmax, kv_l2, matmul_only, no_kv_staging, no_q_load)
+  change the output (tests/test_ablation.py:28-34), on both of the kernel's tile loops
+  (software-pipelined at head_dim 64, one tile at a time otherwise), causal or not, and no_store
+  writes none.
 """
+
+import math
 
 import pytest
 import torch
@@ -87,8 +90,10 @@ def test_scale_first_changes_only_rounding():
 
 
 @pytest.mark.parametrize("knobs", [{"no_exp": True}, {"no_softmax": True}, {"kv_l2": True},
-                                   {"no_softmax": True, "kv_l2": True}, {"no_kv_staging": True}],
-                         ids=["no_exp", "no_softmax", "kv_l2", "matmul_only", "no_kv_staging"])
+                                   {"no_softmax": True, "kv_l2": True}, {"no_kv_staging": True},
+                                   {"no_q_load": True}],
+                         ids=["no_exp", "no_softmax", "kv_l2", "matmul_only", "no_kv_staging",
+                              "no_q_load"])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype,D", [(torch.float16, 16), (torch.bfloat16, 32),
                                      (torch.float16, 64), (torch.bfloat16, 64),
@@ -102,6 +107,31 @@ def test_knockouts_change_the_output(knobs, causal, dtype, D):
     q, k, v = make_qkv(BATCH, 4, 2, 300, 300, D, dtype)
     out = _ablate()(q, k, v, causal=causal, **knobs)
     assert not torch.equal(out, attention(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 64), (torch.bfloat16, 128)])
+def test_no_store_writes_nothing(causal, dtype, D):
+    """The no_store knockout computes every program and writes no output: a sentinel-filled
+    output stays as it was."""
+    import ctypes
+
+    from ablation import ablate_lib
+    from fa2 import _lib
+    from fa2.kernel import LOG2E
+
+    q, k, v = make_qkv(BATCH, 4, 2, 300, 300, D, dtype)
+    out = torch.full_like(q, 3.0)
+    lib = ablate_lib()
+    B, H_q, N, _ = q.shape
+    rc = lib.fa2_ablate_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                 *[_lib._strides(t) for t in (q, k, v, out)], B, H_q, k.shape[1],
+                                 N, N, D, _lib.DTYPE_CODE[dtype], int(causal), 1,
+                                 LOG2E / math.sqrt(D), 2048,  # FA2_ABLATE_NO_STORE
+                                 torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.fa2_ablate_last_error().decode()
+    torch.cuda.synchronize()
+    assert bool((out == 3.0).all())
 
 
 @pytest.mark.parametrize("dtype,D,causal", [(torch.bfloat16, 128, True), (torch.float16, 64, False)])

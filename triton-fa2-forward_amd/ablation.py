@@ -24,6 +24,10 @@ never loads. The reference's variants (bench/ablation.py:1-20, 42-53):
   split_keys       8 waves per program in two groups over the two halves of its key range,
                    merged through LDS, one workgroup per CU (head_dim 128; still attention; not in
                    the reference): what halving the longest program's path buys
+  no_q_load        Q is not read from memory (a lane pattern instead; output wrong on purpose;
+                   not in the reference): what a program's Q load costs
+  no_store         the output is not written (output wrong on purpose; not in the reference):
+                   what a program's store costs
   pack             copy with GQA head packing forced on
   static_order     copy without the dynamic tail of causal grids: workgroup b runs program b
                    (not in the reference; what the run-time dealing of the last programs buys)
@@ -58,7 +62,8 @@ ABLATE_LIB_PATH = os.path.join(HERE, "libfa2_ablate.so")
 
 # switch -> VARIANT bit (FA2_ABLATE_* in include/fa2_ablate.h)
 SWITCH_BITS = {"scale_first": 1, "mask_every_tile": 2, "no_exp": 8, "no_softmax": 16, "kv_l2": 32,
-               "static_order": 128, "no_kv_staging": 256, "split_keys": 512}
+               "static_order": 128, "no_kv_staging": 256, "split_keys": 512, "no_q_load": 1024,
+               "no_store": 2048}
 KNOBS = tuple(SWITCH_BITS)
 VARIANTS = {
     "copy": (),
@@ -71,6 +76,8 @@ VARIANTS = {
     "matmul_only": ("no_softmax", "kv_l2"),
     "no_kv_staging": ("no_kv_staging",),
     "split_keys": ("split_keys",),
+    "no_q_load": ("no_q_load",),
+    "no_store": ("no_store",),
     "pack": ("pack",),
     "static_order": ("static_order",),
 }

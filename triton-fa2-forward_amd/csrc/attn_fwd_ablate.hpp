@@ -24,6 +24,8 @@ constexpr int kAblationVariants[] = {
     kVariantNoSoftmax | kVariantKvL2,             // matmul_only
     kVariantNoKvStaging,                          // no_kv_staging (not in the reference)
     kVariantSplitKeys,                            // split_keys (not in the reference)
+    kVariantNoQLoad,                              // no_q_load (not in the reference)
+    kVariantNoStore,                              // no_store (not in the reference)
     kVariantTimeline,                             // copy + per-workgroup timeline records
 };
 

@@ -50,11 +50,12 @@ int launch_attn_fwd_ablate(const Params& p, int variant, bool causal, unsigned g
   return dispatch<DT, D, kAblationVariants[0], kAblationVariants[1], kAblationVariants[2],
                   kAblationVariants[3], kAblationVariants[4], kAblationVariants[5],
                   kAblationVariants[6], kAblationVariants[7], kAblationVariants[8],
-                  kAblationVariants[9], kAblationVariants[10]>(
+                  kAblationVariants[9], kAblationVariants[10], kAblationVariants[11],
+                  kAblationVariants[12]>(
       p, variant, causal, grid, s, stop);
 }
 
-static_assert(sizeof(kAblationVariants) / sizeof(int) == 11, "dispatch lists every variant");
+static_assert(sizeof(kAblationVariants) / sizeof(int) == 13, "dispatch lists every variant");
 
 template int launch_attn_fwd_ablate<FA2_DT, FA2_D>(const Params&, int, bool, unsigned,
                                                    hipStream_t, hipEvent_t);

@@ -57,6 +57,11 @@ constexpr int kVariantNoKvStaging = 256;
 // per workgroup, in two groups that take the two halves of each program's key range with K/V
 // buffers of their own, and merge through LDS (one workgroup per CU).
 constexpr int kVariantSplitKeys = 512;
+// A program's fixed cost, knocked out: Q is not loaded (a lane pattern in its place), or the
+// output is not stored (the accumulators only kept alive). What hiding a program's Q load or its
+// store behind another program's tiles could gain at most. Outputs wrong by design.
+constexpr int kVariantNoQLoad = 1024;
+constexpr int kVariantNoStore = 2048;
 // Measurement library only, and computes the product's attention: every workgroup also records
 // its timeline (Params::timeline, kTimelineWords words); waits for its stores before the last stamp.
 constexpr int kVariantTimeline = 64;

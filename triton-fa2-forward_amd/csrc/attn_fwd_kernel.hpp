@@ -48,6 +48,13 @@
 #ifndef FA2_FP16_ROUNDED_SUM
 #define FA2_FP16_ROUNDED_SUM 0
 #endif
+// Output store of the one-tile loop at head_dim 128 (unpacked rows, no split-KV): 0 writes each
+// lane's 16-byte pieces straight from the accumulators (every store instruction touches 32 rows),
+// 1 stages the wave's 32 rows through LDS first, so that every store instruction writes 4 whole
+// rows. Compile-time so that an A/B of two builds can compare them (ab.py).
+#ifndef FA2_STAGED_STORE
+#define FA2_STAGED_STORE 0
+#endif
 
 namespace fa2 {
 
@@ -86,6 +93,8 @@ void attn_fwd_kernel(const Params p) {
   constexpr bool kNoSoftmax = (VARIANT & kVariantNoSoftmax) != 0;
   constexpr bool kKvL2 = (VARIANT & kVariantKvL2) != 0;
   constexpr bool kNoKvStaging = (VARIANT & kVariantNoKvStaging) != 0;
+  constexpr bool kNoQLoad = (VARIANT & kVariantNoQLoad) != 0;
+  constexpr bool kNoStore = (VARIANT & kVariantNoStore) != 0;
   constexpr bool kTimeline = (VARIANT & kVariantTimeline) != 0;
   // Measurement library only: the workgroup's waves form two groups of NW / 2 that run the same
   // rows over the two halves of the program's key range, each group with K/V buffers of its own,
@@ -149,8 +158,14 @@ void attn_fwd_kernel(const Params p) {
   {
     const uint16_t* qrow = p.q + pr.b * p.sqb + head * p.sqh + (int64_t)pos * p.sqn + 8 * g;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qreg[ks] = row_ok ? *(const u32x4*)(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (kNoQLoad) {  // knockout: a lane pattern of small values instead of Q
+        const uint32_t w = 0x3c003c00u ^ (uint32_t)(lane * 0x00110011u + ks * 0x00050005u);
+        qreg[ks] = u32x4{w, w ^ 0x00030003u, w ^ 0x00090009u, w ^ 0x000f000fu};
+      } else {
+        qreg[ks] = row_ok ? *(const u32x4*)(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
   }
 
   // ---- key range (fa2/kernel.py:150-175). Tiles below full_end need no mask:
@@ -827,7 +842,50 @@ void attn_fwd_kernel(const Params p) {
   // one division per row, then multiplies: a per-element fp32 division expands to ~11 VALU
   // instructions (64 per lane at head_dim 128, ~1.6 us per wave in every program's epilogue)
   const float inv_l = 1.0f / l;
-  if (row_ok) {
+  // Staged store: after the loop's last barrier no wave reads the last tile's K buffer or the
+  // other V buffer (the next tiles' loads into them were never issued), so the 32 KiB they hold
+  // give each wave 8 KiB of its own. A wave writes its 32 rows there (row-major, 16-byte chunks
+  // XOR-swizzled by row: conflict-free both ways), reads them back four whole rows per
+  // instruction and stores those; no other wave is involved, so no barrier.
+  constexpr bool kStagedStore = FA2_STAGED_STORE && D == 128 && BN == 64 && NW == 4 && !kPipelined &&
+                                !kSplit && !kNoStore;
+  if (kStagedStore && p.splits == 1 && p.pack == 1) {
+    const int last = (n_iter - 1) & 1;
+    u32x4 FA2_LDS* reg = (gwave < 2 ? (u32x4 FA2_LDS*)k_lds[0][last]
+                                    : (u32x4 FA2_LDS*)v_lds[0][last ^ 1]) + (gwave & 1) * 512;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int q = 4 * db + 2 * h + g;  // this lane's dims 8 q .. 8 q + 7 of row c
+        reg[c * 16 + (q ^ (c & 15))] =
+            u32x4{E::pack2(acc[db][8 * h + 0] * inv_l, acc[db][8 * h + 1] * inv_l),
+                  E::pack2(acc[db][8 * h + 2] * inv_l, acc[db][8 * h + 3] * inv_l),
+                  E::pack2(acc[db][8 * h + 4] * inv_l, acc[db][8 * h + 5] * inv_l),
+                  E::pack2(acc[db][8 * h + 6] * inv_l, acc[db][8 * h + 7] * inv_l)};
+      }
+    const int qq = lane & 15;
+    const int wave_row0 = gwave * 32;
+    const int pos0 = pr.tile * p.block_m + wave_row0;  // unpacked: a row's index is its position
+    char* obase = (char*)(p.o + pr.b * p.sob + pr.hq0 * p.soh) + qq * 16;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int r = 4 * k + (lane >> 4);
+      const u32x4 v = reg[r * 16 + (qq ^ (r & 15))];
+      if (wave_row0 + r < p.block_m && pos0 + r < p.n_q)
+        *(u32x4*)(obase + (int64_t)(pos0 + r) * p.son * 2) = v;
+    }
+    if (p.lse && g == 0 && row_ok) {
+      const int64_t row_index = ((int64_t)pr.b * p.h_q + head) * p.n_q + pos;
+      p.lse[row_index] = (m_i + log2f(lx)) * kLn2;
+    }
+  } else if constexpr (kNoStore) {  // knockout: keep the results alive, store nothing
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) asm volatile("" ::"v"(acc[db][i] * inv_l));
+    asm volatile("" ::"v"(lx), "v"(m_i));
+  } else if (row_ok) {
     const int64_t row_index = ((int64_t)pr.b * p.h_q + head) * p.n_q + pos;  // in [B, H_q, N_q]
     // log2 of this row's sum of the weights O is normalised by (exp2(s * qk_scale) rounded to
     // the input type) and of the exact exp2(s * qk_scale), over the keys seen; m is their
