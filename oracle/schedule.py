@@ -29,6 +29,7 @@ import numpy as np
 KCUS, KXCDS, KMAX_XCDS = 256, 8, 16
 CHUNK_KV_BYTES = 8 << 20
 TAIL_PRIVATE_PCT = 0   # the shipped policy; builds can differ (FA2_TAIL_PRIVATE_PCT)
+XCD_REVERSE = True     # the shipped order; builds can differ (FA2_XCD_REVERSE)
 
 
 def make_topology(cus, xcds):
@@ -104,6 +105,12 @@ def program_of(blocks, *, causal, h_q, group, pack, n_tiles, n_bh, unit_chunk, x
         if causal:
             cu = unit_chunk if (unit_chunk > 0 and upx % unit_chunk == 0) else upx
             per_chunk = cu * ppk * n_tiles
+            cpx = cus >> xcd_shift
+            per_xcd = upx * ppk * n_tiles
+            if XCD_REVERSE and per_xcd <= 2 * cpx:
+                sel = slot >= cpx
+                back = cpx + (per_xcd - 1 - slot) if plant != "reverse" else cpx + (per_xcd - slot)
+                slot = np.where(sel, back, slot)
             ch = slot // per_chunk
             rs = slot - ch * per_chunk
             per_t = cu * ppk

@@ -161,7 +161,7 @@ def test_planted_mistakes_fail_the_coverage_check(shapes, plant):
     """The exactly-once check must see an off-by-one in the unit chunk, the reversed second round
     or the tail's private blocks (per-XCD queues, as a 50% build plans them): each planted in
     the restatement fails on the sweep."""
-    failed = 0
+    failed = {True: 0, False: 0}   # by order: XCD-aware (units split over the XCDs) or fallback
     for shape in shapes:
         B, hq, hkv, n, d, causal, pack, bm, cus, xcds, static = shape
         plan, progs, tail_blocks = restated(shape, plant=plant, private_pct=50)
@@ -170,8 +170,26 @@ def test_planted_mistakes_fail_the_coverage_check(shapes, plant):
         else:
             run = progs
         if sch.coverage_errors(run, B, hq, pack, plan["n_tiles"]):
-            failed += 1
-    assert failed > 0, plant
+            failed[(B * hkv) % (1 << plan["xcd_shift"]) == 0] += 1
+    assert failed[True] > 0, plant
+    if plant == "reverse":   # the reversed second slots exist in both orders
+        assert failed[False] > 0, plant
+
+
+@needs_ablate
+@pytest.mark.parametrize("shape", [(1, 32, 8, 2048, 128, 1, 1, 128), (2, 16, 16, 2048, 128, 1, 1, 128),
+                                   (4, 16, 16, 1024, 128, 1, 1, 128), (1, 32, 8, 2048, 64, 1, 1, 128)])
+def test_one_round_causal_grids_pair_heavy_with_light(shape):
+    """What the reversed second slots are for: on a causal grid of at most two programs per CU,
+    the two workgroups that meet on one CU (blocks b and b + 256 on MI355X) run q tiles t and
+    n_tiles - 1 - t, so every CU gets the same number of key tiles (XCD-aware order: the units
+    split over the 8 XCDs)."""
+    fn = _map_fn()
+    got, info = library_map(fn, shape + (256, 8, 0))
+    assert info["tail_wgs"] == 0 and info["grid"] <= 512, info
+    n_tiles = info["n_tiles"]
+    first, second = got[:256, 0], got[256:info["grid"], 0]
+    assert (first[: len(second)] + second == n_tiles - 1).all(), shape
 
 
 def test_restatement_is_exact_without_plants(shapes):

@@ -17,6 +17,14 @@
 
 #define FA2_HD __host__ __device__ __forceinline__
 
+// 1: causal grids of at most two programs per CU in the XCD-aware order reverse the second
+// program of every CU, as grids of at most three in the fallback order do (below); 0: only the
+// fallback order does.
+// Compile-time so that an A/B of two builds can compare them (ab.py).
+#ifndef FA2_XCD_REVERSE
+#define FA2_XCD_REVERSE 1
+#endif
+
 namespace fa2 {
 
 FA2_HD int sched_min(int a, int b) { return a < b ? a : b; }
@@ -44,7 +52,16 @@ FA2_HD int sched_min(int a, int b) { return a < b ? a : b; }
 //     every CU (blocks cus .. 2 cus - 1) is taken in reverse, so the heaviest programs share
 //     their CU with the lightest of the first round: +2.6% on C5 (672 programs), +6% on its
 //     head_dim-64 twin, +3.6% at 384 programs; from 896 programs on it no longer pays (+0.7%,
-//     -1.1% at 1344).
+//     -1.1% at 1344). The hardware fills every CU's first slot before any second one, so the
+//     blocks b and b + cus meet on one CU (the timelines show it).
+//   * The same holds inside each XCD of the XCD-aware causal order: its programs are dealt to
+//     the XCD's CUs a slot at a time (XCD-local slots s and s + CUs per XCD meet on one CU), and
+//     q-tile-major order puts tile t beside tile t - (CUs per XCD) / (programs per q tile). On an
+//     XCD holding at most two programs per CU its second slots are taken in reverse too. Measured
+//     on MI355X against the plain order (same box, interleaved builds): B1 H32/8 N2048 D128 +4.4%
+//     (bf16) and +4.3% (fp16), N1536 +3.1%, B2 H16 N2048 +4.3%, B4 H16 N1024 +3.4%, B1 H16
+//     N4096 +4.5%, fp16 head_dim 64 B1 H32/8 N2048 +2.9% and H24/8 +1.2%; from 2.5 programs per
+//     CU to 3 it did not pay (-1.1% to +0.2%), hence the bound of two.
 struct Program {
   int tile, b, hq0, hkv;
 };
@@ -57,11 +74,17 @@ FA2_HD Program program_of(const Params& p, int block) {
   const int xcds = 1 << p.xcd_shift;
   int kv_index, t, h_in;
   if ((units & (xcds - 1)) == 0) {
-    const int xcd = block & (xcds - 1), slot = block >> p.xcd_shift;
+    const int xcd = block & (xcds - 1), slot0 = block >> p.xcd_shift;
     const int upx = units >> p.xcd_shift;      // units per XCD
     if (CAUSAL) {
       const int cu = (p.unit_chunk > 0 && upx % p.unit_chunk == 0) ? p.unit_chunk : upx;
       const int per_chunk = cu * progs_per_kv * p.n_tiles;  // programs of one chunk
+      int slot = slot0;
+      if (FA2_XCD_REVERSE) {
+        const int cpx = p.cus >> p.xcd_shift;  // CUs per XCD
+        const int per_xcd = upx * progs_per_kv * p.n_tiles;
+        if (per_xcd <= 2 * cpx && slot >= cpx) slot = cpx + (per_xcd - 1 - slot);
+      }
       const int ch = slot / per_chunk;
       const int rs = slot - ch * per_chunk;
       const int per_t = cu * progs_per_kv;     // programs per q tile of one chunk
@@ -71,8 +94,8 @@ FA2_HD Program program_of(const Params& p, int block) {
       h_in = r % progs_per_kv;
     } else {
       const int per_u = p.n_tiles * progs_per_kv;  // programs of one unit
-      const int u = slot / per_u;
-      const int r = slot - u * per_u;
+      const int u = slot0 / per_u;
+      const int r = slot0 - u * per_u;
       t = r / progs_per_kv;
       h_in = r - t * progs_per_kv;
       kv_index = xcd * upx + u;
