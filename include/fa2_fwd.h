@@ -165,11 +165,11 @@ FA2_API size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int3
  * fa2_workspace_bytes_for - the workspace fa2_attn_fwd_ex can use for this launch:
  * fa2_workspace_bytes(...) plus, where the key-norm pass pays for itself, room for its table
  * (one float per batch, kv head and 64 keys). It pays, as measured on MI355X, for bf16 at
- * head_dim 128 (causal or not) and at 64 without the causal mask, when the attention does at
- * least 16384 FLOP per byte of K and at least 2^37 FLOP: the pass reads K once and saves the
- * per-tile row max (2-4% of the kernel). fp16 is left out: its bound (P within fp16's range)
- * fails on unit-variance scores, and the pass then costs 1-3%. No counterpart in the
- * reference. Host policy only.
+ * head_dim 128 (causal or not) and for fp16 or bf16 at 64 without the causal mask, when the
+ * attention does at least 16384 FLOP per byte of K and at least 2^37 FLOP: the pass reads K once
+ * and saves the per-tile row max (2-4% of the kernel). fp16 at head_dim 128 and causal fp16 at
+ * 64 are left out: there the pass and the table's instance cost 1-4% more than they save. No
+ * counterpart in the reference. Host policy only.
  */
 FA2_API size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
                                        int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,

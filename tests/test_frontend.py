@@ -291,9 +291,9 @@ def test_workspace_bytes():
 @needs_lib
 def test_workspace_bytes_for_adds_the_key_table_where_it_pays():
     """The key-norm table (one fp32 per batch, kv head and 64 keys, 256-byte rounded) is asked
-    for on bf16 at head_dim 128, or 64 without the causal mask, when the attention does >= 16384
-    FLOP per byte of K and >= 2^37 FLOP: C3 qualifies; C2 (4097 FLOP/B), C5 (2.2e10 FLOP), the
-    fp16 C4 and the few-queries shapes do not."""
+    for on bf16 at head_dim 128, or (fp16 or bf16) at 64 without the causal mask, when the
+    attention does >= 16384 FLOP per byte of K and >= 2^37 FLOP: C3 and C4 qualify; C2 (4097
+    FLOP/B), C5 (2.2e10 FLOP), fp16 at head_dim 128 and the few-queries shapes do not."""
     lib = _lib.lib()
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     table = lambda B, H_kv, N_kv: up(B * H_kv * -(-N_kv // 64) * 4)  # noqa: E731
@@ -301,7 +301,8 @@ def test_workspace_bytes_for_adds_the_key_table_where_it_pays():
     F16, BF16 = 0, 1
     assert f(1, 32, 8, 8192, 8192, 128, BF16, 1, 1) == table(1, 8, 8192)          # C3
     assert f(1, 32, 8, 8192, 8192, 128, F16, 1, 1) == 0                           # fp16: no
-    assert f(2, 16, 16, 16384, 16384, 64, F16, 0, 1) == 0                         # C4 (fp16)
+    assert f(2, 16, 16, 16384, 16384, 64, F16, 0, 1) == table(2, 16, 16384)       # C4 (fp16)
+    assert f(2, 16, 16, 16384, 16384, 64, F16, 1, 1) == 0                         # causal D64: no
     assert f(2, 16, 16, 16384, 16384, 64, BF16, 0, 1) == table(2, 16, 16384)      # bf16 full D64
     assert f(1, 32, 8, 8192, 8192, 64, BF16, 1, 1) == 0                           # causal D64: no
     assert f(4, 16, 16, 4096, 4096, 128, BF16, 1, 1) == 0                         # C2

@@ -31,6 +31,19 @@ constexpr float kRescaleTau = 8.0f;
 // and l and O stay far from fp32 overflow (l <= 2^32 per key).
 template <int DT>
 constexpr float kBoundTau = DT == 1 ? 32.0f : 15.0f;
+// A row whose bound exceeds m + tau by at most this much skips too: its reference is raised by
+// the next whole number (to bound - tau or just above it) before its first P, so P <= 2^tau
+// still holds and the row's largest P is at least 2^-lift. A whole number scales every P by an
+// exact power of two, so P's rounding to the input type is unchanged (a row of one key still
+// gets its value exactly) until fp16's subnormal range: fp16 keeps full precision down to 2^-14
+// of the new reference instead of the old one (4 bits less range below the row's largest P, whose
+// rounding error stays ~2^-21 of it per key), and bf16 has fp32's exponent range. Compile-time
+// switch FA2_BOUND_LIFT (1 on, 0 off) so that an A/B of two builds can compare them (ab.py).
+#ifndef FA2_BOUND_LIFT
+#define FA2_BOUND_LIFT 1
+#endif
+template <int DT>
+constexpr float kBoundLift = FA2_BOUND_LIFT ? (DT == 1 ? 8.0f : 4.0f) : 0.0f;
 // qk_scale raised by 2^-10: covers the fp32 rounding of the squared norms and of the MFMA's
 // score sums (at most ~2^-17 relative at head_dim 128) in the bound |q| |k|max qk_scale.
 __host__ __device__ constexpr float qk_scale_bound(float qk_scale) {

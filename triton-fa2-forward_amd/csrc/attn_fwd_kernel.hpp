@@ -248,8 +248,10 @@ void attn_fwd_kernel(const Params p) {
   };
   float bound = INFINITY;
   // Set after a row's first tile: no later score of the row can exceed its reference max by
-  // more than kBoundTau<DT>, so its reference never moves again (a NaN bound or reference fails
-  // the test). skip_max: every row of the wave is so, and the wave skips the row max.
+  // more than kBoundTau<DT> (the reference raised by a whole number, to bound - tau or just
+  // above, where the bound was within kBoundLift<DT> of that), so its reference never moves
+  // again (a NaN bound or reference fails the test). skip_max: every row of the wave is so, and
+  // the wave skips the row max.
   bool skip_row = false;
   bool skip_max = false;
 
@@ -492,7 +494,8 @@ void attn_fwd_kernel(const Params p) {
           m_i = m_new;
         }
         if (KB && j == 0) {
-          skip_row = bound <= m_i + kBoundTau<DT>;
+          skip_row = bound <= m_i + (kBoundTau<DT> + kBoundLift<DT>);
+          if (skip_row) m_i += fmaxf(0.f, ceilf(bound - kBoundTau<DT> - m_i));  // O, l still 0
           skip_max = __builtin_amdgcn_ballot_w64(!skip_row) == 0;
         }
       }
@@ -764,7 +767,8 @@ void attn_fwd_kernel(const Params p) {
       m_i = m_new;  // O and l are still zero
       if constexpr (KB) {
         bound = bound_from_table();
-        skip_row = bound <= m_i + kBoundTau<DT>;
+        skip_row = bound <= m_i + (kBoundTau<DT> + kBoundLift<DT>);
+        if (skip_row) m_i += fmaxf(0.f, ceilf(bound - kBoundTau<DT> - m_i));
         skip_max = __builtin_amdgcn_ballot_w64(!skip_row) == 0;
       }
 #pragma unroll
