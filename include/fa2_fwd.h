@@ -167,9 +167,10 @@ FA2_API size_t fa2_workspace_bytes(int32_t batch, int32_t h_q, int32_t n_q, int3
  * (one float per batch, kv head and 64 keys). It pays, as measured on MI355X, for bf16 at
  * head_dim 128 (causal or not) and for fp16 or bf16 at 64 without the causal mask, when the
  * attention does at least 16384 FLOP per byte of K and at least 2^37 FLOP: the pass reads K once
- * and saves the per-tile row max (2-4% of the kernel). fp16 at head_dim 128 and causal fp16 at
- * 64 are left out: there the pass and the table's instance cost 1-4% more than they save. No
- * counterpart in the reference. Host policy only.
+ * and saves the per-tile row max (2-4% of the kernel; fp16 full attention at 64 on
+ * unit-variance data loses under 1%). fp16 at head_dim 128 and causal fp16 at 64 are left out:
+ * there the pass and the table's instance cost 1-4% more than they save. No counterpart in the
+ * reference. Host policy only.
  */
 FA2_API size_t fa2_workspace_bytes_for(int32_t batch, int32_t h_q, int32_t h_kv, int32_t n_q,
                                        int32_t n_kv, int32_t head_dim, int32_t dtype, int32_t causal,

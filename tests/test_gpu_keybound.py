@@ -5,7 +5,8 @@ every 64 keys of every (batch, kv head)) and the kernel instance that uses it: a
 tile, |q| max|k| qk_scale <= m + tau (Cauchy-Schwarz) proves that no later score passes the
 row's reference max m by more than tau (15 for fp16, 32 for bf16, in exp2 units), and waves
 whose rows all pass skip the per-tile row max. A row whose bound passes m + tau by at most the
-lift (4 for fp16, 8 for bf16) skips as well, with its reference raised to bound - tau. attention() asks for the table only on long
+lift (4 for fp16 where the bound is at most 19, 8 for bf16) skips as well, with its reference
+raised by a whole number to bound - tau or just above. attention() asks for the table only on long
 problems (fa2_workspace_bytes_for); these tests force it on small ones by passing the room.
 
 Checked here: the table itself against torch's norms; the output against the oracle with the
@@ -111,14 +112,16 @@ def test_key_bound_rows_that_fail_keep_the_row_max(dtype, causal):
     check_against_oracle(q, k, v, causal, precision=torch.float32, ours=out)
 
 
-@pytest.mark.parametrize("D,causal", [(64, False), (128, True), (128, False)])
-def test_key_bound_lifted_rows_match_oracle(D, causal):
-    """fp16, unit-variance inputs: many rows' bounds land just past tau (15) above their first
-    tile's maximum. Those rows still skip: their reference is raised to bound - 15 before their
-    first P (at most 4 above the first tile's maximum, kBoundLift), so P <= 2^15 holds. The test
-    first checks on the host that such rows exist, then the output against the fp32 oracle."""
-    B, H_q, H_kv, N = 2, 8, 2, 1024
+@pytest.mark.parametrize("D,causal,N,scale", [(64, False, 4096, 1.0), (64, True, 2048, 1.0),
+                                               (128, True, 1024, 0.9), (128, False, 1024, 0.9)])
+def test_key_bound_lifted_rows_match_oracle(D, causal, N, scale):
+    """fp16: rows whose bound lands just past tau (15) above their first tile's maximum still
+    skip, with their reference raised by a whole number (at most 4, kBoundLift) so that
+    P <= 2^15 holds, where the bound is at most 19 (kBoundLiftMax: no P below 2^-24). The test
+    first finds such rows on the host, then checks the output against the fp32 oracle."""
+    B, H_q, H_kv = 2, 8, 2
     q, k, v = make_qkv(B, H_q, H_kv, N, N, D, torch.float16, seed=5)
+    q = (q.float() * scale).to(torch.float16)
     qk = 1.0 / math.sqrt(D) * 1.4426950408889634
     qf, kf = q.float(), k.float().repeat_interleave(H_q // H_kv, dim=1)
     s0 = (qf @ kf[:, :, :64].transpose(-1, -2)) * qk                    # first tile's scores
@@ -131,8 +134,8 @@ def test_key_bound_lifted_rows_match_oracle(D, causal):
     else:
         kmax = kn2.amax(-1, keepdim=True).expand(B, H_q, N)
     bound = (qf.pow(2).sum(-1) * kmax).sqrt() * qk * (1 + 2 ** -10)
-    lift = bound - 15.0 - m0
-    lifted = int(((lift > 0) & (lift <= 4)).sum().item())
+    lift = torch.ceil(bound - 15.0 - m0)
+    lifted = int(((lift > 0) & (lift <= 4) & (bound <= 19.0)).sum().item())
     print(f"fp16 D={D} causal={causal}: {lifted} of {B * H_q * N} rows lifted", flush=True)
     assert lifted >= 32
     out, _, _ = run_with_table(q, k, v, causal)

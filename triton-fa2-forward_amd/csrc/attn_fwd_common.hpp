@@ -35,15 +35,23 @@ constexpr float kBoundTau = DT == 1 ? 32.0f : 15.0f;
 // the next whole number (to bound - tau or just above it) before its first P, so P <= 2^tau
 // still holds and the row's largest P is at least 2^-lift. A whole number scales every P by an
 // exact power of two, so P's rounding to the input type is unchanged (a row of one key still
-// gets its value exactly) until fp16's subnormal range: fp16 keeps full precision down to 2^-14
-// of the new reference instead of the old one (4 bits less range below the row's largest P, whose
-// rounding error stays ~2^-21 of it per key), and bf16 has fp32's exponent range. Compile-time
-// switch FA2_BOUND_LIFT (1 on, 0 off) so that an A/B of two builds can compare them (ab.py).
+// gets its value exactly) until fp16's subnormal range, which then starts up to 4 binades nearer
+// the row's largest P (keys there are rounded to 2^-25 absolute instead of 2^-29 of it); bf16
+// has fp32's exponent range. Compile-time switch FA2_BOUND_LIFT (1 on, 0 off) so that an A/B of
+// two builds can compare them (ab.py).
 #ifndef FA2_BOUND_LIFT
 #define FA2_BOUND_LIFT 1
 #endif
+#ifndef FA2_BOUND_LIFT_F16
+#define FA2_BOUND_LIFT_F16 4
+#endif
 template <int DT>
-constexpr float kBoundLift = FA2_BOUND_LIFT ? (DT == 1 ? 8.0f : 4.0f) : 0.0f;
+constexpr float kBoundLift = FA2_BOUND_LIFT ? (DT == 1 ? 8.0f : (float)FA2_BOUND_LIFT_F16) : 0.0f;
+// ... and only rows whose bound is at most this: every score of the row lies in [-bound, bound],
+// and a lifted reference is at most bound - tau + 1, so P >= 2^(-2 bound + tau - 1) >= 2^-24,
+// fp16's smallest subnormal: no key's weight vanishes that the unlifted row would keep.
+template <int DT>
+constexpr float kBoundLiftMax = DT == 1 ? INFINITY : (kBoundTau<DT> + 23.0f) / 2.0f;
 // qk_scale raised by 2^-10: covers the fp32 rounding of the squared norms and of the MFMA's
 // score sums (at most ~2^-17 relative at head_dim 128) in the bound |q| |k|max qk_scale.
 __host__ __device__ constexpr float qk_scale_bound(float qk_scale) {

@@ -88,10 +88,10 @@ size_t key_table_bytes(int64_t batch, int64_t h_kv, int64_t n_kv) {
 // launch) and saves the per-tile row max where the bound holds. Measured on MI355X against the
 // same launch without the table (N(0,1) inputs unless stated):
 //   bf16 D128 causal +1.4% (C3 +1.3-2.2%), bf16 D128 full +0.3%, bf16 D64 full +3.7-4.0%,
-//   bf16 D64 causal -0.9%. fp16, whose tau (15, the fp16 range of P) is tighter, gained most of
-//   its unit-variance rows back with the reference lift (kBoundLift): D64 full +3.0% at unit and
-//   at C4's half scale (before the lift -1.3-3.0% at unit scale), D64 causal -4.0% (-4.2% at half
-//   scale), D128 causal -2.1%, D128 full -1.5%.
+//   bf16 D64 causal -0.9%. fp16, whose tau (15, the fp16 range of P) is tighter: D64 full +2.6%
+//   at C4's half scale and -0.5% to -0.8% at unit scale with the reference lift (kBoundLift,
+//   limited to bounds that keep every P above fp16's smallest subnormal; -1.3% to -3.0% without
+//   it), D64 causal -4.0% (-3.5% at half scale), D128 causal -1.6%, D128 full -1.2%.
 // Hence: head_dim 128 (bf16) or full attention at 64 (both types), and only where the attention
 // does >= 16384 FLOP per byte of K and >= 2^37 FLOP (the pass's cost against the ~2-4% it can
 // save).

@@ -494,7 +494,8 @@ void attn_fwd_kernel(const Params p) {
           m_i = m_new;
         }
         if (KB && j == 0) {
-          skip_row = bound <= m_i + (kBoundTau<DT> + kBoundLift<DT>);
+          const float lift = bound <= kBoundLiftMax<DT> ? kBoundLift<DT> : 0.f;
+          skip_row = bound <= m_i + (kBoundTau<DT> + lift);
           if (skip_row) m_i += fmaxf(0.f, ceilf(bound - kBoundTau<DT> - m_i));  // O, l still 0
           skip_max = __builtin_amdgcn_ballot_w64(!skip_row) == 0;
         }
@@ -767,7 +768,8 @@ void attn_fwd_kernel(const Params p) {
       m_i = m_new;  // O and l are still zero
       if constexpr (KB) {
         bound = bound_from_table();
-        skip_row = bound <= m_i + (kBoundTau<DT> + kBoundLift<DT>);
+        const float lift = bound <= kBoundLiftMax<DT> ? kBoundLift<DT> : 0.f;
+        skip_row = bound <= m_i + (kBoundTau<DT> + lift);
         if (skip_row) m_i += fmaxf(0.f, ceilf(bound - kBoundTau<DT> - m_i));
         skip_max = __builtin_amdgcn_ballot_w64(!skip_row) == 0;
       }
