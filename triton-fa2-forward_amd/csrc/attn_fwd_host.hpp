@@ -128,8 +128,13 @@ Topology make_topology(int cus, int xcds) {
 // ~kChunkKvBytes of units. Measured on MI355X against all of the XCD's units at once (causal,
 // bf16 unless stated; 2, 3 or 4 units per chunk): B8 H16 N4096 D128 +4.9% (4), B2 H32 N8192
 // D128 +2.4% (2), C2 (B4 H16 N4096) +0.5% (4); at head_dim 64 (fp16 B4 H16 N4096) chunks of 4
-// and 2 lost 4% and 9%, which the byte budget avoids (1 MiB units: all 8 at once).
-constexpr int64_t kChunkKvBytes = int64_t(8) << 20;
+// and 2 lost 4% and 9%, which the byte budget avoids (1 MiB units: all 8 at once). Budgets of
+// 2, 4 and 16 MiB against 8 (FA2_CHUNK_KV_MIB, compile-time so that ab.py can compare builds):
+// 8 is the best or tied on every shape measured (C2: 4 MiB +1.1% time, 2 MiB +12%).
+#ifndef FA2_CHUNK_KV_MIB
+#define FA2_CHUNK_KV_MIB 8
+#endif
+constexpr int64_t kChunkKvBytes = int64_t(FA2_CHUNK_KV_MIB) << 20;
 int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim, const Topology& topo) {
   const int64_t upx = units >> topo.xcd_shift;
   if (upx < 1) return 1;
