@@ -24,6 +24,11 @@
 #ifndef FA2_XCD_REVERSE
 #define FA2_XCD_REVERSE 1
 #endif
+// 1: the fallback order reverses the second program of every CU on causal grids of at most three
+// programs per CU (below); 0: it does not. Compile-time, for ab.py.
+#ifndef FA2_FALLBACK_REVERSE
+#define FA2_FALLBACK_REVERSE 1
+#endif
 
 namespace fa2 {
 
@@ -102,7 +107,7 @@ FA2_HD Program program_of(const Params& p, int block) {
     }
   } else {
     const int grid = p.n_tiles * p.n_bh;
-    if (CAUSAL && grid <= 3 * p.cus && block >= p.cus) {
+    if (FA2_FALLBACK_REVERSE && CAUSAL && grid <= 3 * p.cus && block >= p.cus) {
       const int end = sched_min(grid, 2 * p.cus);
       if (block < end) block = p.cus + (end - 1 - block);
     }
