@@ -169,6 +169,11 @@ int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim, const Topology
 #ifndef FA2_TAIL_EXTRA_PCT
 #define FA2_TAIL_EXTRA_PCT 6
 #endif
+// ... and the fewest programs per XCD, in percent of the workgroups the XCD holds at once, for a
+// grid to get a tail (200: two rounds)
+#ifndef FA2_TAIL_MIN_ROUNDS_PCT
+#define FA2_TAIL_MIN_ROUNDS_PCT 200
+#endif
 
 // Dynamic tail of causal grids. Each XCD's programs run in a static order (program_of), but the
 // XCDs do not run at one speed: their clocks differ by up to ~10% under the chip's power limit,
@@ -183,7 +188,8 @@ int32_t unit_chunk(int64_t units, int64_t n_kv, int64_t head_dim, const Topology
 // whose units do not split over the XCDs (program_of's fallback order; a quarter of every XCD's
 // blocks): B3 H28/4 N4096 +1.2%, N8192 +1.9%, B1 H20/4 N8192 +2.7%. Non-causal grids (every
 // program the same work, so no light programs to even out the end) lost 0.3% and keep the static
-// order; so do grids of fewer than two rounds per XCD.
+// order; so do grids of fewer than two rounds per XCD (FA2_TAIL_MIN_ROUNDS_PCT: a tail from one
+// or 1.25 rounds cost C5 1.6% and moved the other grids of one to two rounds within noise).
 // One shared counter hands a program to whichever XCD asks, so its unit's K/V is fetched into a
 // second L2 (C3's reads past L2 rose from 213.6 to 334.1 MB per launch). A build with
 // FA2_TAIL_PRIVATE_PCT > 0 gives each XCD of the XCD-aware order a queue of its own: the heavier
@@ -213,7 +219,7 @@ TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, in
     // program_of's fallback order (q tile outermost, heaviest first; the hardware still deals
     // block b to XCD b % xcds): the last quarter of every XCD's blocks, and the remainder
     const int64_t per_xcd = grid / xcds;
-    if (per_xcd < 2 * slots) return s;
+    if (per_xcd * 100 < FA2_TAIL_MIN_ROUNDS_PCT * slots) return s;
     const int64_t static_blocks =
         (per_xcd - (per_xcd * FA2_TAIL_SHARE_PCT + 99) / 100) * xcds;
     s.static_blocks = (int32_t)static_blocks;
@@ -223,7 +229,7 @@ TailSchedule tail_schedule(bool causal, int splits, int waves, int64_t units, in
   }
   const int64_t upx = units / xcds;
   const int64_t per_xcd = upx * progs_per_kv * n_tiles;
-  if (per_xcd < 2 * slots) return s;
+  if (per_xcd * 100 < FA2_TAIL_MIN_ROUNDS_PCT * slots) return s;
   const int64_t cu = (chunk > 0 && upx % chunk == 0) ? chunk : upx;  // program_of's chunk
   const int64_t tail = std::min((per_xcd * FA2_TAIL_SHARE_PCT + 99) / 100,
                                 cu * progs_per_kv * n_tiles * FA2_TAIL_CHUNK_PCT / 100);
