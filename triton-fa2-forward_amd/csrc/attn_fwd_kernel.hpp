@@ -55,6 +55,12 @@
 #ifndef FA2_STAGED_STORE
 #define FA2_STAGED_STORE 0
 #endif
+// Q, read once per program, and the output, written once: 1 loads / stores them non-temporally
+// (bit 0: Q, bit 1: O), so that they take less of L2 from the K/V tiles that programs share.
+// Compile-time so that an A/B of two builds can compare them (ab.py).
+#ifndef FA2_NT_QO
+#define FA2_NT_QO 0
+#endif
 
 namespace fa2 {
 
@@ -163,7 +169,11 @@ void attn_fwd_kernel(const Params p) {
         const uint32_t w = 0x3c003c00u ^ (uint32_t)(lane * 0x00110011u + ks * 0x00050005u);
         qreg[ks] = u32x4{w, w ^ 0x00030003u, w ^ 0x00090009u, w ^ 0x000f000fu};
       } else {
-        qreg[ks] = row_ok ? *(const u32x4*)(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+        if constexpr ((FA2_NT_QO & 1) != 0)
+          qreg[ks] = row_ok ? __builtin_nontemporal_load((const u32x4*)(qrow + 16 * ks))
+                            : u32x4{0u, 0u, 0u, 0u};
+        else
+          qreg[ks] = row_ok ? *(const u32x4*)(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
@@ -933,7 +943,10 @@ void attn_fwd_kernel(const Params p) {
                              E::pack2(acc[db][8 * h + 2] * inv_l, acc[db][8 * h + 3] * inv_l),
                              E::pack2(acc[db][8 * h + 4] * inv_l, acc[db][8 * h + 5] * inv_l),
                              E::pack2(acc[db][8 * h + 6] * inv_l, acc[db][8 * h + 7] * inv_l)};
-            *(u32x4*)(orow + d0) = o;
+            if constexpr ((FA2_NT_QO & 2) != 0)
+              __builtin_nontemporal_store(o, (u32x4*)(orow + d0));
+            else
+              *(u32x4*)(orow + d0) = o;
           }
         }
       if (p.lse && g == 0) p.lse[row_index] = lse2_exact * kLn2;
