@@ -566,8 +566,9 @@ def test_build_records_the_resources_of_every_product_instance():
 @needs_lib
 def test_default_instances_keep_the_occupancy_the_design_counts_on():
     """The compiler's report of the default instances: two waves per SIMD and no VGPR spills at
-    head_dim 128 (C2, C3, C5; with and without the key-norm table), three waves per SIMD and no
-    VGPR spills for the fp16 head_dim-64 software-pipelined instance (C4)."""
+    head_dim 128 (C2, C3, C5; with and without the key-norm table), three waves per SIMD for the
+    fp16 head_dim-64 software-pipelined instances (C4), whose rounded P sum costs a few spilled
+    VGPRs (at most 5; tests/test_gpu_determinism.py runs every spilling instance)."""
     import sweep
 
     res = sweep.load_resources()
@@ -576,8 +577,9 @@ def test_default_instances_keep_the_occupancy_the_design_counts_on():
             for keynorm in (False, True):
                 r = res[sweep.instance_name(dt, 128, 128, 64, causal, keynorm)]
                 assert r["waves_per_simd"] >= 2 and r["vgpr_spills"] == 0, r
-    r = res[sweep.instance_name(0, 64, 128, 64, False, False)]
-    assert r["waves_per_simd"] == 3 and r["vgpr_spills"] == 0, r
+    for keynorm in (False, True):
+        r = res[sweep.instance_name(0, 64, 128, 64, False, keynorm)]
+        assert r["waves_per_simd"] == 3 and r["vgpr_spills"] <= 5, r
 
 
 @needs_lib

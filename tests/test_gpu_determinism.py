@@ -3,7 +3,7 @@
 The compiler's resource report (fa2/kernel_resources.json, written by csrc/build.py) shows VGPR
 spills to scratch in the head_dim-64 software-pipelined instances held to three waves per SIMD:
 bf16 causal and full (2-3 VGPRs, 12-16 bytes per lane), their key-norm instances (4-5, 20-24
-bytes), and the fp16 key-norm instances (1-2, 8-12 bytes). Scratch loads and stores count in the
+bytes), and the fp16 ones (2-5 VGPRs, with and without the key-norm table: the rounded P sum). Scratch loads and stores count in the
 same vmcnt counter as the kernel's hand-placed LDS-DMA waits, so a wrong count would show up as a
 read of K/V or of a spilled value before it landed: the output would then change from launch to
 launch. Each case below runs a full-size grid (C4-sized for full attention, C2-sized for causal)
@@ -32,6 +32,8 @@ CASES = [
     ("bf16_d64_causal", torch.bfloat16, True, False, (4, 16, 4096)),
     ("bf16_d64_full_keynorm", torch.bfloat16, False, True, (2, 16, 16384)),
     ("bf16_d64_causal_keynorm", torch.bfloat16, True, True, (4, 16, 4096)),
+    ("fp16_d64_full", torch.float16, False, False, (2, 16, 16384)),
+    ("fp16_d64_causal", torch.float16, True, False, (4, 16, 4096)),
     ("fp16_d64_full_keynorm", torch.float16, False, True, (2, 16, 16384)),
     ("fp16_d64_causal_keynorm", torch.float16, True, True, (4, 16, 4096)),
 ]

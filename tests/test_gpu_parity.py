@@ -356,3 +356,21 @@ def test_grid_beyond_65535_programs(B, H, causal):
     and the program decomposition in both orders (units a multiple of 8 XCDs or not)."""
     q, k, v = make_qkv(B, H, H, 16, 16, 64, torch.float16)
     check_against_oracle(q, k, v, causal)
+
+
+@pytest.mark.parametrize("N,scale,seed,D", [(16384, 3.0, 5, 64), (4096, 4.0, 11, 64),
+                                            (4096, 4.0, 11, 32), (8192, 3.0, 9, 128)])
+def test_peaky_fp16_rows_stay_within_the_rule(N, scale, seed, D):
+    """fp16 with q and k scaled x3-x4 (scores of a few units' spread: rows dominated by one or a
+    few keys). With the lazy reference max a row's largest P is 2^x, x up to 8, not 1, and its
+    fp16 rounding reaches the output unless l sums the same rounded P the PV product uses:
+    with an fp32 sum of the unrounded P, head_dim 64 reached 2.07x SDPA's error here (seed 5,
+    N 16384), past the reference's 2x rule."""
+    from fa2.kernel import attention
+
+    print(f"peaky fp16: B=1 H=4 N={N} D={D} scale={scale} seed={seed}", flush=True)
+    q, k, v = make_qkv(1, 4, 4, N, N, D, torch.float16, seed=seed)
+    q = (q.float() * scale).to(torch.float16)
+    k = (k.float() * scale).to(torch.float16)
+    out = attention(q, k, v, causal=False)
+    check_against_oracle(q, k, v, False, precision=torch.float32, ours=out)

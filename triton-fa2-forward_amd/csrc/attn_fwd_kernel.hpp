@@ -43,10 +43,10 @@
 #include "attn_fwd_common.hpp"
 #include "attn_fwd_schedule.hpp"
 
-// fp16 below head_dim 128 sums l from the unrounded P in fp32 (0) or from P rounded to fp16 with
-// v_dot2 (1); compile-time so that an A/B of two builds can compare them (ab.py).
+// fp16 below head_dim 128 sums l from P rounded to fp16 with v_dot2 (1) or from the unrounded P
+// in fp32 (0); compile-time so that an A/B of two builds can compare them (ab.py).
 #ifndef FA2_FP16_ROUNDED_SUM
-#define FA2_FP16_ROUNDED_SUM 0
+#define FA2_FP16_ROUNDED_SUM 1
 #endif
 // Output store of the one-tile loop at head_dim 128 (unpacked rows, no split-KV): 0 writes each
 // lane's 16-byte pieces straight from the accumulators (every store instruction touches 32 rows),
@@ -362,11 +362,12 @@ void attn_fwd_kernel(const Params p) {
   // convex combination of V rows. With the lazy reference max a row's largest P is 2^x, not 1,
   // and its bf16 rounding (2^-9) would otherwise reach a row dominated by one key in full
   // (C5's outlier keys: 1.74x SDPA's error with the fp32 sum, 0.93x with this one). l_exact then
-  // sums the unrounded P for the log-sum-exp output. fp16 rounds P 8x finer, so either sum is
-  // accurate there; the rounded one (v_dot2, half the instructions) is faster at head_dim 128
-  // (+2.5% on C3's shape) and the fp32 one, as in the reference (fa2/kernel.py:98), at 64 and
-  // below (C4: 9% faster; with it the fp16 pipelined loop needs 160 VGPRs, three waves per
-  // SIMD, with the rounded sum 173, two).
+  // sums the unrounded P for the log-sum-exp output. fp16 rounds P 8x finer, but the same holds
+  // on peaky rows: a row's largest P is 2^x with x up to tau, not 1, and its fp16 rounding reached
+  // the output with the fp32 sum (fp16 head_dim 64 full attention, inputs x2 to x4: 1.5-2.07x
+  // SDPA's error; with the rounded sum 1.0-1.2x). So fp16 sums the rounded P too, at every head
+  // dim (the fp32 sum, as in the reference, fa2/kernel.py:98, ran 1.6-2.2% faster at head_dim 64
+  // and below: the rounded one spills 2-5 VGPRs in the pipelined loop's three waves per SIMD).
   constexpr bool kRoundedSum = DT == 1 || D == 128 || FA2_FP16_ROUNDED_SUM;
   float m_i = -INFINITY;
   float l_i = 0.f;
