@@ -594,7 +594,17 @@ void attn_fwd_kernel(const Params p) {
     constexpr int NPV = NT * DB;                        // MFMAs of the PV product
     constexpr int LA_V = NPV < 4 ? NPV : 4;             // PV MFMAs whose V operands are read ahead
     constexpr int KREAD_EVERY = NPV / (LA * NB) > 0 ? NPV / (LA * NB) : 1;
-    constexpr int kVpm = 10, kEpm = 4;                  // VALU / exp instructions per S MFMA
+#ifndef FA2_PIPE_VPM
+#define FA2_PIPE_VPM 0
+#endif
+    // VALU / exp instructions per S MFMA: the tile's softmax VALU work over its 8 S MFMAs (per
+    // lane 32 FMAs and 16 conversions, plus 32 adds for the fp32 sum or 16 v_dot2 for the rounded
+    // one: 80 or 64 instructions). Measured with the rounded sum (same box, interleaved builds;
+    // FA2_PIPE_VPM): 7 is best for the key-norm instances (C4 +1.4% over 8, bf16 full +1.2%), 8
+    // for the others (fp16 causal +1.0% over 7); 10, the fp32 sum's 80 / 8, spilled and ran 1-2%
+    // slower with the rounded sum.
+    constexpr int kVpm = FA2_PIPE_VPM ? FA2_PIPE_VPM : (kRoundedSum ? (KB ? 7 : 8) : 10);
+    constexpr int kEpm = 4;
     u32x4 kop[LA][NB];
     float m_new = -INFINITY;
 
