@@ -435,6 +435,10 @@ def test_measurement_library_rejects_unbuilt_variants_before_any_launch():
     rc = lib.fa2_ablate_attn_fwd(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
                                  32, 48, 0, 1, 1, 0.18, 8, None)
     assert rc == -1 and b"head_dim" in lib.fa2_ablate_last_error()
+    # the key split (512) is built at head_dim 128 only
+    rc = lib.fa2_ablate_attn_fwd(0x1000, 0x2000, 0x3000, 0x4000, st, st, st, st, 1, 4, 4, 32,
+                                 32, 64, 0, 1, 1, 0.18, 512, None)
+    assert rc == -1 and b"key split" in lib.fa2_ablate_last_error()
 
 
 @needs_ablate

@@ -248,6 +248,9 @@ def measure_shape(args, N):
         if name == "pack" and (group == 1 or 128 % group):
             print(f"(pack skipped: GQA group {group} does not pack into 128-row programs)")
             continue
+        if name == "split_keys" and args.head_dim != 128:
+            print(f"(split_keys skipped: built at head_dim 128 only, not {args.head_dim})")
+            continue
         launchers[name] = launcher(name, q, k, v, causal)
         outputs[name] = launchers[name]()
     torch.cuda.synchronize()

@@ -69,6 +69,10 @@ int fa2_ablate_attn_fwd(const void* q, const void* k, const void* v, void* out,
     return fail(FA2_EINVAL, "variant 0x%x is not one of the built timing variants",
                 (unsigned)variant);
   }
+  if ((variant & fa2::kVariantSplitKeys) && head_dim != 128) {
+    g_err[0] = '\0';
+    return fail(FA2_EINVAL, "the key split is built at head_dim 128 only, got %d", head_dim);
+  }
   const LaunchArgs a{q, k, v, out, q_stride, k_stride, v_stride, o_stride, batch, h_q, h_kv,
                      n_q, n_kv, head_dim, dtype, causal, pack, 128, 0, qk_scale, nullptr, 1,
                      nullptr, 0, variant, nullptr, 0, static_order};
