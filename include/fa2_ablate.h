@@ -117,6 +117,8 @@ FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, voi
 #define FA2_ABLATE_CEIL_MFMA_EXP 4          /* random, registers, one exp2 per MFMA          */
 #define FA2_ABLATE_CEIL_MFMA_FMA2 5         /* random, registers, two FMAs per MFMA          */
 #define FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC 6  /* mode 3 with the accumulators in VGPRs    */
+#define FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC 7  /* mode 6, one 1 KiB read per two MFMAs     */
+#define FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE 8  /* mode 7, one wave per SIMD           */
 #define FA2_ABLATE_CEIL_MAX_WORKGROUPS 65536
 #define FA2_ABLATE_CEIL_MAX_ITERS 100000
 
@@ -127,7 +129,9 @@ FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, voi
  * the per-MFMA extra work of `mode` (FA2_ABLATE_CEIL_*) on independent data. One launch does
  * workgroups x 4 x iters x 16 x 32768 FLOP. The chip lowers its clock to hold its power limit,
  * and an MFMA's energy depends on its operands, so the rate depends on the mode and on how long
- * it runs; time it back to back for a second or more. No counterpart in the reference: a
+ * it runs; time it back to back for a second or more. Modes 7 and 8 price the operand reads of
+ * 64-row waves (each K/V operand read feeds two MFMAs); mode 8 launches 128 KiB of LDS per
+ * workgroup, so one workgroup (one wave per SIMD) per CU. No counterpart in the reference: a
  * measurement tool for the roofline's practical ceiling. out: device memory, 4-byte aligned,
  * at least workgroups x 256 floats (out_words); its values mean nothing. FA2_EINVAL for a
  * mode, workgroup or iteration count out of range, before any launch.

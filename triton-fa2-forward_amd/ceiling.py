@@ -20,6 +20,10 @@ amdsmi sampling the clock and the socket power:
   mfma_fma2         random, registers, two FMAs per MFMA    } MFMAs, against two FMAs
   mfma_lds_softmax_vacc  mfma_lds_softmax with the accumulators in VGPRs, as the attention
                     kernel holds them (the compiler puts the other modes' in AGPRs)
+  half_lds_softmax_vacc  that with one 1 KiB read per two MFMAs: the operand reads of 64-row
+                    waves, whose K and V operands each feed two 32-row blocks' MFMAs
+  half_lds_softmax_vacc_1wave  the same at one wave per SIMD (128 KiB of LDS per workgroup,
+                    one workgroup per CU), the occupancy of 64-row waves at head_dim 128
 
 Per mode: TFLOP/s, the median graphics clock and power, TFLOP/s per GHz (the issue efficiency,
 whatever the clock: the peak is 1048.6 per GHz) and the fraction of the 2.4 GHz peak.
@@ -41,7 +45,8 @@ sys.path.insert(0, HERE)
 sys.path.insert(0, os.path.dirname(HERE))
 
 MODES = {"mfma": 0, "mfma_const": 1, "mfma_lds": 2, "mfma_lds_softmax": 3,  # FA2_ABLATE_CEIL_*
-         "mfma_exp": 4, "mfma_fma2": 5, "mfma_lds_softmax_vacc": 6}
+         "mfma_exp": 4, "mfma_fma2": 5, "mfma_lds_softmax_vacc": 6,
+         "half_lds_softmax_vacc": 7, "half_lds_softmax_vacc_1wave": 8}
 PEAK_TFLOPS = 2516.6            # 256 CUs x 4096 FLOP/clk x 2.4 GHz (dense bf16/fp16)
 PEAK_MHZ = 2400.0
 MFMA_FLOP = 32 * 32 * 16 * 2    # one v_mfma_f32_32x32x16_bf16

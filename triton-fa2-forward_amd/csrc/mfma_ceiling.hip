@@ -19,6 +19,12 @@
 //   FA2_ABLATE_CEIL_MFMA_FMA2         random operands in registers, two FMAs per MFMA
 //   FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC  the LDS_SOFTMAX mix with the two accumulators held in
 //                                     VGPRs, where the attention kernel holds its own
+//   FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC  the VACC mix with one 1 KiB read per two MFMAs: the
+//                                     operand reads of 64-row waves, where every K and V
+//                                     operand feeds the MFMAs of two 32-row blocks
+//   FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE  the same with 128 KiB of LDS per workgroup: one
+//                                     workgroup, one wave per SIMD, per CU (the occupancy that
+//                                     64-row waves at head_dim 128 would have)
 // (EXP and FMA2 price an exp2 against FMAs in the issue cycles beside the MFMAs). For every other
 // mode the compiler keeps the accumulators in AGPRs, since nothing but MFMAs touches them in the
 // loop; with vector work beside the MFMAs the two placements do not issue alike, so VACC gives
@@ -69,7 +75,9 @@ template <int MODE>
 __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, int iters) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr bool kRandom = MODE != FA2_ABLATE_CEIL_MFMA_CONST;
-  constexpr bool kVacc = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC;
+  constexpr bool kHalf = MODE == FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC ||
+                        MODE == FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE;
+  constexpr bool kVacc = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC || kHalf;
   constexpr bool kLds = MODE == FA2_ABLATE_CEIL_MFMA_LDS ||
                         MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX || kVacc;
   constexpr bool kSoftmax = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX || kVacc;
@@ -96,18 +104,25 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
+      // the operand of MFMA i: a[i & 3], or a[(i >> 1) & 3] when every read feeds two MFMAs
+      constexpr int kShift = kHalf ? 1 : 0;
+      const int ai = (i >> kShift) & 3;
       if constexpr (kVacc) {
         f32x16& acc = (i & 1) ? acc1 : acc0;
         asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
                      : "+v"(acc)
-                     : "v"(a[i & 3]), "v"(b));
+                     : "v"(a[ai]), "v"(b));
       } else if (i & 1) {
-        acc1 = Elem<1>::mma(a[i & 3], b, acc1);
+        acc1 = Elem<1>::mma(a[ai], b, acc1);
       } else {
-        acc0 = Elem<1>::mma(a[i & 3], b, acc0);
+        acc0 = Elem<1>::mma(a[ai], b, acc0);
       }
-      // the read for the MFMA four ahead, into the register just consumed
-      if constexpr (kLds) a[i & 3] = *(const volatile u32x4 FA2_LDS*)(chunks + ((i + 4) & 15) * 1024);
+      // the read for the operand four ahead, into the register just consumed (after its last
+      // MFMA)
+      if constexpr (kLds) {
+        if (!kHalf || (i & 1))
+          a[ai] = *(const volatile u32x4 FA2_LDS*)(chunks + (((i >> kShift) + 4) & 15) * 1024);
+      }
       if constexpr (kSoftmax) {
         const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i & 7], 0.0625f, -4.0f));
         sv[i & 7] = e;
@@ -135,8 +150,11 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
 
 template <int MODE>
 int launch_ceiling(float* out, int workgroups, int iters, hipStream_t s) {
-  hipLaunchKernelGGL(mfma_ceiling_kernel<MODE>, dim3(workgroups), dim3(kCeilThreads),
-                     kCeilLdsBytes, s, out, iters);
+  // 128 KiB leaves room for one workgroup per CU (160 KiB of LDS)
+  constexpr size_t lds = MODE == FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE ? 2 * kCeilLdsBytes
+                                                                             : kCeilLdsBytes;
+  hipLaunchKernelGGL(mfma_ceiling_kernel<MODE>, dim3(workgroups), dim3(kCeilThreads), lds, s,
+                     out, iters);
   return (int)hipGetLastError();
 }
 
@@ -176,6 +194,10 @@ int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStre
       return launch_ceiling<FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC>(out, workgroups, iters, s);
     case FA2_ABLATE_CEIL_MFMA_FMA2:
       return launch_ceiling<FA2_ABLATE_CEIL_MFMA_FMA2>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC:
+      return launch_ceiling<FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE:
+      return launch_ceiling<FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE>(out, workgroups, iters, s);
     default: return (int)hipErrorInvalidValue;
   }
 }
