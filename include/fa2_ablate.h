@@ -117,7 +117,7 @@ FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, voi
 #define FA2_ABLATE_CEIL_MFMA_EXP 4          /* random, registers, one exp2 per MFMA          */
 #define FA2_ABLATE_CEIL_MFMA_FMA2 5         /* random, registers, two FMAs per MFMA          */
 #define FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC 6  /* mode 3 with the accumulators in VGPRs    */
-#define FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC 7  /* mode 6, one 1 KiB read per two MFMAs     */
+#define FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC 7  /* mode 6, one read per two MFMAs, 4 accs  */
 #define FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE 8  /* mode 7, one wave per SIMD           */
 #define FA2_ABLATE_CEIL_MAX_WORKGROUPS 65536
 #define FA2_ABLATE_CEIL_MAX_ITERS 100000

@@ -21,7 +21,8 @@ amdsmi sampling the clock and the socket power:
   mfma_lds_softmax_vacc  mfma_lds_softmax with the accumulators in VGPRs, as the attention
                     kernel holds them (the compiler puts the other modes' in AGPRs)
   half_lds_softmax_vacc  that with one 1 KiB read per two MFMAs: the operand reads of 64-row
-                    waves, whose K and V operands each feed two 32-row blocks' MFMAs
+                    waves, whose K and V operands each feed two 32-row blocks' MFMAs (four
+                    accumulators, as such a wave has at least that many tiles in flight)
   half_lds_softmax_vacc_1wave  the same at one wave per SIMD (128 KiB of LDS per workgroup,
                     one workgroup per CU), the occupancy of 64-row waves at head_dim 128
 

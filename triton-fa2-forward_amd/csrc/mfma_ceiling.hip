@@ -21,7 +21,8 @@
 //                                     VGPRs, where the attention kernel holds its own
 //   FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC  the VACC mix with one 1 KiB read per two MFMAs: the
 //                                     operand reads of 64-row waves, where every K and V
-//                                     operand feeds the MFMAs of two 32-row blocks
+//                                     operand feeds the MFMAs of two 32-row blocks; four
+//                                     accumulators instead of two
 //   FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE  the same with 128 KiB of LDS per workgroup: one
 //                                     workgroup, one wave per SIMD, per CU (the occupancy that
 //                                     64-row waves at head_dim 128 would have)
@@ -98,9 +99,13 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
 #pragma unroll
   for (int j = 0; j < 8; ++j) sv[j] = (float)(mix32(seed + 8 + j) & 0xffffu) * (1.0f / 65536.0f);
   float lsum = 0.f, eprev = 0.f;
-  f32x16 acc0 = {}, acc1 = {};
-  // 2 wait states between the vector writes of acc0, acc1 and b and the first asm MFMA
-  if constexpr (kVacc) asm volatile("s_nop 1" : "+v"(acc0), "+v"(acc1), "+v"(b));
+  // independent accumulators: two, or four in the half-read modes (a 64-row wave has four S and
+  // eight O tiles in flight, and one wave per SIMD must not wait on one MFMA's result)
+  constexpr int kAcc = kHalf ? 4 : 2;
+  f32x16 acc[4] = {};
+  // 2 wait states between the vector writes of the accumulators and b and the first asm MFMA
+  if constexpr (kVacc)
+    asm volatile("s_nop 1" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(b));
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -108,14 +113,11 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
       constexpr int kShift = kHalf ? 1 : 0;
       const int ai = (i >> kShift) & 3;
       if constexpr (kVacc) {
-        f32x16& acc = (i & 1) ? acc1 : acc0;
         asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
-                     : "+v"(acc)
+                     : "+v"(acc[i % kAcc])
                      : "v"(a[ai]), "v"(b));
-      } else if (i & 1) {
-        acc1 = Elem<1>::mma(a[ai], b, acc1);
       } else {
-        acc0 = Elem<1>::mma(a[ai], b, acc0);
+        acc[i % kAcc] = Elem<1>::mma(a[ai], b, acc[i % kAcc]);
       }
       // the read for the operand four ahead, into the register just consumed (after its last
       // MFMA)
@@ -136,8 +138,10 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
       }
     }
   }
-  if constexpr (kVacc) asm volatile("s_nop 7\n\ts_nop 3" : "+v"(acc0), "+v"(acc1));
-  const f32x16 s = acc0 + acc1;
+  if constexpr (kVacc)
+    asm volatile("s_nop 7\n\ts_nop 3" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+  f32x16 s = acc[0] + acc[1];
+  if constexpr (kAcc == 4) s += acc[2] + acc[3];
   float t = lsum;
   if constexpr (kExp || kFma2) {
 #pragma unroll

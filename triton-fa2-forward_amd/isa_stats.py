@@ -10,8 +10,8 @@ device only; no GPU needed) with the library's own flags, takes one instance of
 attn_fwd_kernel<DT, D, waves, block_n, causal, VARIANT>, and prints:
 
   * its resources from the code object's metadata (VGPRs, AGPRs, SGPRs, spills, LDS);
-  * every loop (a backward branch and the blocks it spans), and for the tile loop (the loop with
-    the most MFMAs) each basic block's instructions by class: a tile runs the blocks on its
+  * every loop (a backward branch and the blocks it spans), and for the tile loop (the innermost
+    loop with the most MFMAs) each basic block's instructions by class: a tile runs the blocks on its
     common path, while the mask, rescale and log-sum-exp blocks run only on some tiles;
   * per block, a cycle budget: matrix-core cycles (a 32x32x16 MFMA keeps its SIMD's matrix core
     busy for 8 passes of 4 clocks, 32 cycles, at the peak rate) against issue cycles (a wave
@@ -169,8 +169,16 @@ def report(asm, name):
         f"{a}-{b} ({sum(1 for i in insts[a:b + 1] if i.startswith('v_mfma'))})" for a, b in lp))
     if not lp:
         return "\n".join(lines), None
-    first, last = max(lp, key=lambda r: (sum(1 for i in insts[r[0]:r[1] + 1]
-                                              if i.startswith("v_mfma")), r[0] - r[1]))
+    def n_mfma(r):
+        return sum(1 for i in insts[r[0]:r[1] + 1] if i.startswith("v_mfma"))
+
+    # The tile loop: the most MFMAs among the innermost loops that hold any. A backward branch
+    # from a block placed after the loop (a rare path jumping back) spans more than the loop,
+    # and the range it spans holds the loop and the prologue's MFMAs too.
+    with_mfma = [r for r in lp if n_mfma(r)]
+    innermost = [r for r in with_mfma
+                 if not any(o != r and r[0] <= o[0] and o[1] <= r[1] for o in with_mfma)]
+    first, last = max(innermost, key=lambda r: (n_mfma(r), r[0] - r[1]))
     lines += ["", f"tile loop: instructions {first}-{last}", "",
               "| block | instructions | mfma | trans | dot | valu | lane move | agpr move | lds | vmem | "
               "salu | wait/sync | control | mfma cycles | issue cycles |",
