@@ -82,3 +82,31 @@ def test_c3_instance_tile_loop_and_resources():
     with_mfma = [bc for _, bc in per_block if bc["mfma"]]
     assert sorted(bc["mfma"] for bc in with_mfma) == [16, 16]
     assert "tile loop" in text
+
+
+def test_the_tile_loop_is_the_innermost_loop_with_mfmas():
+    """A rare block placed after the loop that branches back to an earlier label makes a backward
+    branch spanning the loop and the MFMAs before it; the tile loop is still the inner one."""
+    listing = LISTING.replace("\ts_endpgm\n", "\ts_cbranch_execz .LBB0_9\n\ts_endpgm\n.LBB0_9:\n"
+                              "\tv_mov_b32_e32 v1, 1\n\ts_branch .LBB0_0\n").replace(
+        "; %bb.0:\n", "; %bb.0:\n.LBB0_0:\n\tv_mfma_f32_32x32x16_bf16 v[8:23], v[2:5], v[6:9], v[8:23]\n")
+    insts, labels = parse(function_body(listing, "_kern"))
+    spans = loops(insts, labels)
+    assert len(spans) == 2 and spans[0] == (labels[".LBB0_1"], labels[".LBB0_3"] + 1)
+    text, (_, _, first, last, _) = report(listing, "_kern")
+    assert (first, last) == spans[0], text
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc not installed")
+def test_c4_instance_pipelined_tile_loop():
+    """The instance C4 runs (fp16, head_dim 64, 64-key tiles, full attention, key-norm): the
+    pipelined loop holds two tiles per trip, so its tile loop has 2 x 16 MFMAs, 2 x 32 exp2 plus
+    the rescale factor and 2 x 16 dot2 (the rounded-P sum), at three waves per SIMD (168 VGPRs)."""
+    asm = compile_listing(0, 64)
+    name = kernel_name(0, 64, 4, 64, False, 4)
+    meta = metadata(asm, name)
+    assert meta["vgpr_count"] <= 168, meta
+    text, (insts, labels, first, last, per_block) = report(asm, name)
+    total, _ = histogram(insts[first:last + 1])
+    assert total["mfma"] == 32 and total["trans"] == 65 and total["dot"] == 32, (total, text)
