@@ -619,3 +619,15 @@ def test_fa2_installs_as_a_package(tmp_path):
     assert res.returncode == 0, res.stdout + res.stderr
     kernel_file, version = res.stdout.split("\n")[:2]
     assert kernel_file.startswith(str(target)) and "gfx950" in version
+
+
+def test_ab_library_suffixes():
+    """ab.py's NAME=PATH[@kt|@nt][@bmNNN]: the table mode and the BLOCK_M a build is launched
+    with; a path that merely contains '@bm' keeps it."""
+    import ab
+
+    assert ab.parse_lib_suffixes("lib.so") == ("lib.so", None, 128)
+    assert ab.parse_lib_suffixes("lib.so@kt") == ("lib.so", "kt", 128)
+    assert ab.parse_lib_suffixes("lib.so@nt@bm256") == ("lib.so", "nt", 256)
+    assert ab.parse_lib_suffixes("v/lib.so@bm64") == ("v/lib.so", None, 64)
+    assert ab.parse_lib_suffixes("d@bmx/lib.so") == ("d@bmx/lib.so", None, 128)

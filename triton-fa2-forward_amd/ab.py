@@ -23,7 +23,12 @@ workspace (no key-norm table), a ":kt" suffix a workspace with room for the tabl
 library's policy says (the table then always runs). A library given as NAME=PATH@kt or @nt
 takes that table mode on every workload, so that one build can be timed with and without the
 table in the same rounds (outputs then need not be equal bit for bit: rows that skip the row max
-round differently). Prints one line of JSON per workload, and a table.
+round differently). A further @bmNNN suffix (after the table mode, if any) launches that library
+with BLOCK_M NNN instead of 128 (256: 8-wave programs). With --sustained S, each library then also
+runs alone, back to back, for S seconds with the clock and socket power sampled
+(ablation.sustained_run): work that costs energy also costs clock under the chip's power limit,
+which interleaved rounds, sharing one clock, do not show. Prints one line of JSON per workload,
+and a table.
 """
 
 import argparse
@@ -51,6 +56,18 @@ def load(path):
     return h
 
 
+def parse_lib_suffixes(path):
+    """PATH[@kt|@nt][@bmNNN] -> (PATH, table mode or None, BLOCK_M)."""
+    bm = 128
+    head, sep, tail = path.rpartition("@bm")
+    if sep and tail.isdigit():
+        path, bm = head, int(tail)
+    mode = None
+    if path.endswith("@kt") or path.endswith("@nt"):
+        path, mode = path[:-3], path[-2:]
+    return path, mode, bm
+
+
 def make_workload(spec):
     """(q, k, v, causal, table) for a config name or X:B:Hq:Hkv:N:D:causal:dtype[:scale], with an
     optional ':nt' (table False: no workspace) or ':kt' (table "force") suffix."""
@@ -76,7 +93,7 @@ def make_workload(spec):
     return q, k, v, causal, table
 
 
-def make_call(h, q, k, v, out, causal, table):
+def make_call(h, q, k, v, out, causal, table, block_m=128):
     """A no-argument launch of library `h` on the current stream, as attention() calls it."""
     import torch
 
@@ -96,14 +113,14 @@ def make_call(h, q, k, v, out, causal, table):
 
     def fn():
         rc = h.fa2_attn_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), *strides,
-                               B, Hq, Hkv, Nq, Nkv, D, dt, int(causal), 1, 128, 0, scale, None, 1,
+                               B, Hq, Hkv, Nq, Nkv, D, dt, int(causal), 1, block_m, 0, scale, None, 1,
                                ws.data_ptr() if nb else None, nb, stream)
         if rc:
             raise RuntimeError(h.fa2_last_error().decode())
     return fn
 
 
-def ab(libs, spec, rounds, steps, warmup):
+def ab(libs, spec, rounds, steps, warmup, sustained=0.0):
     """Interleaved rounds over the libraries on one workload; returns the result dict."""
     import torch
 
@@ -114,7 +131,8 @@ def ab(libs, spec, rounds, steps, warmup):
     flops = bench.attn_flops(B, Hq, N, k.shape[2], D, causal)
     outs = {n: torch.empty_like(q) for n in libs}
     modes = {"kt": "force", "nt": False, None: table}
-    fns = {n: make_call(h, q, k, v, outs[n], causal, modes[mode]) for n, (h, mode) in libs.items()}
+    fns = {n: make_call(h, q, k, v, outs[n], causal, modes[mode], bm)
+           for n, (h, mode, bm) in libs.items()}
     names = list(libs)
     first = names[0]
 
@@ -133,6 +151,12 @@ def ab(libs, spec, rounds, steps, warmup):
             ms, _ = bench.time_steps(fns[n], steps, warmup)
             per[n].append(ms / steps)
     after = bit_equal()
+    alone = {}
+    if sustained > 0:
+        from ablation import sustained_run
+
+        for n in names:
+            alone[n] = sustained_run(fns[n], sustained, flops)
     base = statistics.median(per[first])
     res = {}
     for n in names:
@@ -142,6 +166,10 @@ def ab(libs, spec, rounds, steps, warmup):
                   "tflops": round(flops / (med * 1e-3) / 1e12, 1),
                   "vs_first_pct": round(100.0 * (base / med - 1.0), 2),
                   "bit_equal_to_first": same[n] and after[n]}
+        if n in alone:
+            a = alone[n]
+            res[n]["alone"] = {"tflops": round(a["tflops"], 1), "sclk_mhz": a["sclk_mhz"],
+                               "power_w": a["power_w"]}
     del q, k, v, outs, fns
     torch.cuda.empty_cache()
     return res
@@ -154,6 +182,8 @@ def main():
     ap.add_argument("--rounds", type=int, default=8)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--sustained", type=float, default=0.0,
+                    help="also each build alone for this many seconds: its rate, clock and power")
     ap.add_argument("--out", default=None, help="also write the results as JSON here")
     args = ap.parse_args()
 
@@ -162,19 +192,19 @@ def main():
     libs = {}
     for spec in args.libs:
         name, path = spec.split("=", 1)
-        mode = None
-        if path.endswith("@kt") or path.endswith("@nt"):
-            path, mode = path[:-3], path[-2:]
-        libs[name] = (load(path), mode)
+        path, mode, bm = parse_lib_suffixes(path)
+        libs[name] = (load(path), mode, bm)
     results = {}
     for cfg in args.configs:
         print(f"ab: {cfg}, {len(libs)} builds, {args.rounds} rounds x {args.steps} steps", flush=True)
-        res = ab(libs, cfg, args.rounds, args.steps, args.warmup)
+        res = ab(libs, cfg, args.rounds, args.steps, args.warmup, args.sustained)
         results[cfg] = res
         print(json.dumps({"workload": cfg, "builds": res}), flush=True)
         for n, r in res.items():
             print(f"  {cfg:24s} {n:12s} {r['us']:10.2f} us [{r['min_us']:.2f}-{r['max_us']:.2f}] "
-                  f"{r['tflops']:8.1f} TFLOP/s {r['vs_first_pct']:+6.2f}%  same={r['bit_equal_to_first']}",
+                  f"{r['tflops']:8.1f} TFLOP/s {r['vs_first_pct']:+6.2f}%  same={r['bit_equal_to_first']}"
+                  + (f"  alone {r['alone']['tflops']:.1f} TFLOP/s at {r['alone']['sclk_mhz']} MHz, "
+                     f"{r['alone']['power_w']} W" if "alone" in r else ""),
                   flush=True)
     if args.out:
         with open(args.out, "w") as f:

@@ -61,6 +61,12 @@
 #ifndef FA2_NT_QO
 #define FA2_NT_QO 0
 #endif
+// 1: 8-wave (256-row) programs at head_dim 128 run the software-pipelined loop (each wave
+// interleaves its own softmax with its own MFMAs), whose two waves per SIMD come from one
+// workgroup and meet its barrier together; 0: the one-tile loop. Compile-time, for ab.py.
+#ifndef FA2_PIPE_WIDE
+#define FA2_PIPE_WIDE 0
+#endif
 
 namespace fa2 {
 
@@ -381,7 +387,7 @@ void attn_fwd_kernel(const Params p) {
   // The main loop: at head_dim 64 software-pipelined across tiles inside each wave, else
   // one tile at a time with two waves per SIMD overlapping each other (measured per D). The
   // pipelined loop holds two S tiles: at 128-key tiles that spills, so those keep the other.
-  constexpr bool kPipelined = D == 64 && BN <= 64;
+  constexpr bool kPipelined = (D == 64 || (FA2_PIPE_WIDE && D == 128 && NW == 8)) && BN <= 64;
   if constexpr (!kPipelined) {
     // ---- main loop. Per tile j, one barrier, placed between the two products:
     //   S_j = K_j Q^T                      K_j's operands partly read during PV_{j-1}
@@ -603,8 +609,9 @@ void attn_fwd_kernel(const Params p) {
     // FA2_PIPE_VPM): 7 is best for the key-norm instances (C4 +1.4% over 8, bf16 full +1.2%), 8
     // for the others (fp16 causal +1.0% over 7); 10, the fp32 sum's 80 / 8, spilled and ran 1-2%
     // slower with the rounded sum.
-    constexpr int kVpm = FA2_PIPE_VPM ? FA2_PIPE_VPM : (kRoundedSum ? (KB ? 7 : 8) : 10);
-    constexpr int kEpm = 4;
+    constexpr int kVpm = FA2_PIPE_VPM ? FA2_PIPE_VPM
+                                      : D == 128 ? 4 : (kRoundedSum ? (KB ? 7 : 8) : 10);
+    constexpr int kEpm = D == 128 ? 2 : 4;  // 32 exp2 per tile over its KS * NB S MFMAs
     u32x4 kop[LA][NB];
     float m_new = -INFINITY;
 

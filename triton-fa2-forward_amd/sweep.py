@@ -1,7 +1,7 @@
 """Tile-configuration sweep on gfx950 (counterpart of the reference's bench/sweep.py:24-105).
 
     python triton-fa2-forward_amd/sweep.py --config C3 [--block-m 64 128 256] [--block-n 32 64 128]
-                                           [--rounds 5] [--iters 10] [--json out.json]
+                                           [--rounds 5] [--iters 10] [--sustained 2] [--json out.json]
 
 Times every (block_m, block_n) pair on one BASELINE.json workload, interleaved over rounds so
 that clock drift hits all variants alike (the reference's ablation protocol,
@@ -11,6 +11,10 @@ and the compiled resources of the kernel instance that ran it, as the reference'
 registers, spills and shared memory (bench/sweep.py:95-100): VGPRs, AGPRs, SGPRs, VGPR and SGPR
 spills, LDS per workgroup and waves per SIMD, from the compiler's own report of this build
 (fa2/kernel_resources.json, written by csrc/build.py from -Rpass-analysis=kernel-resource-usage).
+With --sustained S, each variant then also runs alone, back to back, for S seconds with the clock
+and socket power sampled (ablation.sustained_run): the chip holds its power limit by lowering the
+clock, so a configuration that stages fewer K/V bytes per FLOP (more rows per workgroup) can gain
+clock that the interleaved rounds, which share one clock between all variants, do not show.
 """
 
 import argparse
@@ -66,6 +70,8 @@ def main():
     ap.add_argument("--block-n", type=int, nargs="+", default=[32, 64, 128])
     ap.add_argument("--rounds", type=int, default=5)
     ap.add_argument("--iters", type=int, default=10)
+    ap.add_argument("--sustained", type=float, default=0.0,
+                    help="also each variant alone for this many seconds: its rate, clock and power")
     ap.add_argument("--json", default=None)
     args = ap.parse_args()
 
@@ -108,6 +114,15 @@ def main():
             torch.cuda.synchronize()
             samples[(bm, bn)].append(s.elapsed_time(e) / args.iters)
         print(f"round {r + 1}/{args.rounds} done", flush=True)
+    sustained = {}
+    if args.sustained > 0:
+        from ablation import sustained_run
+
+        for bm, bn in variants:
+            sustained[(bm, bn)] = sustained_run(
+                lambda: attention(q, k, v, causal=causal, block_m=bm, block_n=bn), args.sustained,
+                flops)
+            print(f"sustained block_m={bm} block_n={bn} done", flush=True)
     resources = load_resources()
     key_table = (_lib.workspace_bytes_for(B, H_q, k.shape[1], N, k.shape[2], D, q.dtype, causal, 1)
                  > _lib.workspace_bytes(B, H_q, N, D, 1))
@@ -117,12 +132,19 @@ def main():
         name = instance_name(_lib.DTYPE_CODE[q.dtype], D, bm, bn, causal, key_table)
         rows.append({"block_m": bm, "block_n": bn, "median_ms": med,
                      "tflops": flops / (med * 1e-3) / 1e12, "samples_ms": ms,
-                     "kernel": name, "resources": resources.get(name)})
+                     "kernel": name, "resources": resources.get(name),
+                     **({"sustained": sustained[(bm, bn)]} if (bm, bn) in sustained else {})})
     rows.sort(key=lambda r: r["median_ms"])
     print(f"{bench.describe(args.config)}: median over {args.rounds} interleaved rounds of {args.iters}")
     for r in rows:
+        su = r.get("sustained")
+        alone = ""
+        if su:
+            ghz = (su["sclk_mhz"] or 0) / 1000.0
+            alone = (f"  alone: {su['tflops']:7.1f} TFLOP/s at {su['sclk_mhz']} MHz, {su['power_w']} W"
+                     + (f", {su['tflops'] / ghz:.1f} per GHz" if ghz else ""))
         print(f"  block_m={r['block_m']:4d} block_n={r['block_n']:4d}  {r['median_ms']:8.4f} ms  "
-              f"{r['tflops']:7.1f} TFLOP/s  {resource_text(r['resources'])}", flush=True)
+              f"{r['tflops']:7.1f} TFLOP/s  {resource_text(r['resources'])}{alone}", flush=True)
     if args.json:
         with open(args.json, "w") as f:
             json.dump({"config": args.config, "rows": rows}, f, indent=1)
