@@ -119,6 +119,8 @@ FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, voi
 #define FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC 6  /* mode 3 with the accumulators in VGPRs    */
 #define FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC 7  /* mode 6, one read per two MFMAs, 4 accs  */
 #define FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE 8  /* mode 7, one wave per SIMD           */
+#define FA2_ABLATE_CEIL_LDS_SOFTMAX64_VACC_3WAVE 9  /* mode 6 with head_dim 64's softmax per MFMA,
+                                                       three waves per SIMD                    */
 #define FA2_ABLATE_CEIL_MAX_WORKGROUPS 65536
 #define FA2_ABLATE_CEIL_MAX_ITERS 100000
 
@@ -131,7 +133,9 @@ FA2_API int fa2_ablate_timeline(const void* q, const void* k, const void* v, voi
  * and an MFMA's energy depends on its operands, so the rate depends on the mode and on how long
  * it runs; time it back to back for a second or more. Modes 7 and 8 price the operand reads of
  * 64-row waves (each K/V operand read feeds two MFMAs); mode 8 launches 128 KiB of LDS per
- * workgroup, so one workgroup (one wave per SIMD) per CU. No counterpart in the reference: a
+ * workgroup, so one workgroup (one wave per SIMD) per CU. Mode 9 is the head_dim-64 kernel's mix
+ * (two scores, two exp2, one pack and one dot2 per MFMA) at its occupancy: 48 KiB of LDS per
+ * workgroup, three workgroups (three waves per SIMD) per CU. No counterpart in the reference: a
  * measurement tool for the roofline's practical ceiling. out: device memory, 4-byte aligned,
  * at least workgroups x 256 floats (out_words); its values mean nothing. FA2_EINVAL for a
  * mode, workgroup or iteration count out of range, before any launch.

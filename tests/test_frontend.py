@@ -470,7 +470,7 @@ def test_mfma_ceiling_rejects_bad_arguments_before_any_launch():
 
     lib, fn = ceiling._fn()
     for mode, wg, it, out, words, code, msg in (
-            (-1, 8, 1, 0x1000, 2048, -1, b"mode"), (9, 8, 1, 0x1000, 2048, -1, b"mode"),
+            (-1, 8, 1, 0x1000, 2048, -1, b"mode"), (10, 8, 1, 0x1000, 2048, -1, b"mode"),
             (0, 0, 1, 0x1000, 2048, -1, b"workgroups"), (0, 65537, 1, 0x1000, 1 << 30, -1, b"workgroups"),
             (0, 8, 0, 0x1000, 2048, -1, b"iters"), (3, 8, 100001, 0x1000, 2048, -1, b"iters"),
             (0, 8, 1, None, 2048, -1, b"null"), (1, 8, 1, 0x1002, 2048, -2, b"aligned"),
@@ -489,7 +489,7 @@ def test_mfma_ceiling_rejects_bad_arguments_before_any_launch():
             (0x1000, 1024, 0x2000, 511, 2, -1, b"512")):
         rc = rd(src, nb, out, words, wg, None)
         assert rc == code and msg in lib.fa2_ablate_last_error(), (src, nb, rc, lib.fa2_ablate_last_error())
-    assert list(ceiling.MODES.values()) == [0, 1, 2, 3, 4, 5, 6, 7, 8]
+    assert list(ceiling.MODES.values()) == [0, 1, 2, 3, 4, 5, 6, 7, 8, 9]
 
 
 def test_ablation_front_end_checks_arguments_on_the_cpu():

@@ -25,6 +25,8 @@ amdsmi sampling the clock and the socket power:
                     accumulators, as such a wave has at least that many tiles in flight)
   half_lds_softmax_vacc_1wave  the same at one wave per SIMD (128 KiB of LDS per workgroup,
                     one workgroup per CU), the occupancy of 64-row waves at head_dim 128
+  lds_softmax64_vacc_3wave  mfma_lds_softmax_vacc with head_dim 64's softmax per MFMA (two FMAs,
+                    two exp2, one pack, one dot2) at three waves per SIMD (48 KiB of LDS each)
 
 Per mode: TFLOP/s, the median graphics clock and power, TFLOP/s per GHz (the issue efficiency,
 whatever the clock: the peak is 1048.6 per GHz) and the fraction of the 2.4 GHz peak.
@@ -47,11 +49,14 @@ sys.path.insert(0, os.path.dirname(HERE))
 
 MODES = {"mfma": 0, "mfma_const": 1, "mfma_lds": 2, "mfma_lds_softmax": 3,  # FA2_ABLATE_CEIL_*
          "mfma_exp": 4, "mfma_fma2": 5, "mfma_lds_softmax_vacc": 6,
-         "half_lds_softmax_vacc": 7, "half_lds_softmax_vacc_1wave": 8}
+         "half_lds_softmax_vacc": 7, "half_lds_softmax_vacc_1wave": 8,
+         "lds_softmax64_vacc_3wave": 9}
 PEAK_TFLOPS = 2516.6            # 256 CUs x 4096 FLOP/clk x 2.4 GHz (dense bf16/fp16)
 PEAK_MHZ = 2400.0
 MFMA_FLOP = 32 * 32 * 16 * 2    # one v_mfma_f32_32x32x16_bf16
 WORKGROUPS = 2048               # 8 per CU: four rounds of the two resident workgroups
+# three resident workgroups per CU: 9 per CU, three whole rounds
+WORKGROUPS_BY_MODE = {"lds_softmax64_vacc_3wave": 2304}
 ITERS = 6000                    # 16 MFMAs each: ~10 ms per launch at ~1900 TFLOP/s
 
 
@@ -168,7 +173,7 @@ def main():
     print("|---|---|---|---|---|---|")
     rows = {}
     for m in args.modes:
-        r = rows[m] = measure(m, args.seconds)
+        r = rows[m] = measure(m, args.seconds, workgroups=WORKGROUPS_BY_MODE.get(m, WORKGROUPS))
         print(f"| {m} | {r['tflops']:.0f} | {r['sclk_mhz']} | {r['power_w']} | "
               f"{r['tflops_per_ghz']} | {100 * r['frac_of_peak']:.1f} |", flush=True)
     if args.hbm:

@@ -178,7 +178,7 @@ long long fa2_ablate_tail_launches(void) { return g_tail_launches.load(); }
 int fa2_ablate_mfma_ceiling(int32_t mode, int32_t workgroups, int32_t iters, float* out,
                             int64_t out_words, void* stream) {
   g_err[0] = '\0';
-  if (mode < FA2_ABLATE_CEIL_MFMA || mode > FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE)
+  if (mode < FA2_ABLATE_CEIL_MFMA || mode > FA2_ABLATE_CEIL_LDS_SOFTMAX64_VACC_3WAVE)
     return fail(FA2_EINVAL, "unknown ceiling mode %d", (int)mode);
   if (workgroups < 1 || workgroups > FA2_ABLATE_CEIL_MAX_WORKGROUPS)
     return fail(FA2_EINVAL, "workgroups %d outside [1, %d]", (int)workgroups,

@@ -26,6 +26,10 @@
 //   FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE  the same with 128 KiB of LDS per workgroup: one
 //                                     workgroup, one wave per SIMD, per CU (the occupancy that
 //                                     64-row waves at head_dim 128 would have)
+//   FA2_ABLATE_CEIL_LDS_SOFTMAX64_VACC_3WAVE  the VACC mix with head_dim 64's softmax per MFMA (a
+//                                     tile's 16 MFMAs carry its 32 scores per lane: two FMAs, two
+//                                     exp2, one bf16 pack, one dot2 sum) at its occupancy: 48 KiB
+//                                     of LDS, three workgroups (three waves per SIMD) per CU
 // (EXP and FMA2 price an exp2 against FMAs in the issue cycles beside the MFMAs). For every other
 // mode the compiler keeps the accumulators in AGPRs, since nothing but MFMAs touches them in the
 // loop; with vector work beside the MFMAs the two placements do not issue alike, so VACC gives
@@ -78,7 +82,8 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
   constexpr bool kRandom = MODE != FA2_ABLATE_CEIL_MFMA_CONST;
   constexpr bool kHalf = MODE == FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC ||
                         MODE == FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE;
-  constexpr bool kVacc = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC || kHalf;
+  constexpr bool kSm64 = MODE == FA2_ABLATE_CEIL_LDS_SOFTMAX64_VACC_3WAVE;
+  constexpr bool kVacc = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX_VACC || kHalf || kSm64;
   constexpr bool kLds = MODE == FA2_ABLATE_CEIL_MFMA_LDS ||
                         MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX || kVacc;
   constexpr bool kSoftmax = MODE == FA2_ABLATE_CEIL_MFMA_LDS_SOFTMAX || kVacc;
@@ -125,7 +130,13 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
         if (!kHalf || (i & 1))
           a[ai] = *(const volatile u32x4 FA2_LDS*)(chunks + (((i >> kShift) + 4) & 15) * 1024);
       }
-      if constexpr (kSoftmax) {
+      if constexpr (kSm64) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i & 7], 0.0625f, -4.0f));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[(i + 4) & 7], 0.0625f, -4.0f));
+        sv[i & 7] = e0;
+        sv[(i + 4) & 7] = e1;
+        lsum = Elem<1>::sum2(Elem<1>::pack2(e0, e1), lsum);
+      } else if constexpr (kSoftmax) {
         const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i & 7], 0.0625f, -4.0f));
         sv[i & 7] = e;
         if (i & 1) lsum = Elem<1>::sum2(Elem<1>::pack2(eprev, e), lsum);
@@ -155,7 +166,9 @@ __global__ __launch_bounds__(kCeilThreads) void mfma_ceiling_kernel(float* out, 
 template <int MODE>
 int launch_ceiling(float* out, int workgroups, int iters, hipStream_t s) {
   // 128 KiB leaves room for one workgroup per CU (160 KiB of LDS)
+  // (48 KiB: three per CU)
   constexpr size_t lds = MODE == FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE ? 2 * kCeilLdsBytes
+                         : MODE == FA2_ABLATE_CEIL_LDS_SOFTMAX64_VACC_3WAVE ? 48 * 1024
                                                                              : kCeilLdsBytes;
   hipLaunchKernelGGL(mfma_ceiling_kernel<MODE>, dim3(workgroups), dim3(kCeilThreads), lds, s,
                      out, iters);
@@ -202,6 +215,8 @@ int launch_mfma_ceiling(int mode, float* out, int workgroups, int iters, hipStre
       return launch_ceiling<FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC>(out, workgroups, iters, s);
     case FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE:
       return launch_ceiling<FA2_ABLATE_CEIL_HALF_LDS_SOFTMAX_VACC_1WAVE>(out, workgroups, iters, s);
+    case FA2_ABLATE_CEIL_LDS_SOFTMAX64_VACC_3WAVE:
+      return launch_ceiling<FA2_ABLATE_CEIL_LDS_SOFTMAX64_VACC_3WAVE>(out, workgroups, iters, s);
     default: return (int)hipErrorInvalidValue;
   }
 }
